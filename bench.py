@@ -1,0 +1,178 @@
+#!/usr/bin/env python3
+"""MhcPre benchmark on one MI355X: tokens/s and achieved HBM bandwidth.
+
+Workload (default): the headline prefill shape n=4, D=7168, T=8192, bf16 x,
+gamma on -- one "step" is one MhcPre launch over all T rows with every input
+already resident in HBM.  Prints ONE JSON line.
+
+  value      tokens/s = T / (mean launch time over the timed steps)
+  roofline   algorithmic bytes per launch / mean launch time, against 8 TB/s;
+             bytes = x + phi + gamma + bias + alpha + hIn + hPost + hRes, each
+             counted once (hPre is not part of the operator contract)
+  cpu_baseline  the scalar C oracle (reference floating-point order), OpenMP
+             over rows, timed on this host on a bounded row sample of the
+             same inputs
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
+
+WORKLOADS = {
+    # name: (n, D, T, bf16, gamma, outlier rows x50)
+    1: (4, 256, 128, False, False, False),
+    2: (4, 4096, 1024, True, True, False),
+    3: (4, 7168, 8192, True, True, False),
+    4: (8, 7168, 64, False, False, False),
+    5: (8, 8192, 5472, True, True, True),
+}
+METRIC = "MhcPre tokens/s + achieved HBM GB/s (% of peak), n=4 D=7168 T=8192 bf16"
+
+
+def algorithmic_bytes(n: int, D: int, T: int, bf16_or_f16: bool, gamma: bool) -> int:
+    sx = 2
+    M = n * n + 2 * n
+    K = n * D
+    b = T * K * sx + K * M * 4 + (K * 4 if gamma else 0) + M * 4 + 12
+    b += T * D * sx + T * n * 4 + T * n * n * 4
+    return b
+
+
+def make_inputs(cfg: int, device):
+    import torch
+
+    n, D, T, bf16, gamma, outliers = WORKLOADS[cfg]
+    K, M = n * D, n * n + 2 * n
+    gen = torch.Generator(device=device)
+    gen.manual_seed(20261201 + cfg)
+    x = torch.randn((T, n, D), generator=gen, device=device, dtype=torch.float32)
+    if outliers:
+        idx = torch.arange(0, T, 100, device=device)
+        x[idx] *= 50.0
+        x[T - 1] *= 50.0
+    x = x.to(torch.bfloat16 if bf16 else torch.float16)
+    phi = torch.randn((M, K), generator=gen, device=device) * (1.0 / K ** 0.5)
+    bias = torch.rand((M,), generator=gen, device=device) * 0.2 - 0.1
+    alpha = torch.full((3,), 0.01, device=device)
+    g = (1.0 + 0.1 * torch.randn((K,), generator=gen, device=device)) if gamma else None
+    return x, phi.contiguous(), alpha, bias, g
+
+
+def cpu_baseline(x, phi, alpha, bias, gamma, bf16: bool, target_s: float) -> dict:
+    """Time the C oracle on a row sample of the same inputs (all host cores)."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as orc
+
+    T = x.shape[0]
+    threads = orc.max_threads()
+    phi_h = phi.cpu().numpy()
+    alpha_h, bias_h = alpha.cpu().numpy(), bias.cpu().numpy()
+    g_h = gamma.cpu().numpy() if gamma is not None else None
+
+    def run(rows: int) -> float:
+        xs = x[:rows].view(torch.int16).cpu().numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        orc.mhc_pre(xs, bf16, phi_h, alpha_h, bias_h, g_h, nthreads=threads)
+        return time.perf_counter() - t0
+
+    probe = max(threads, 8)
+    dt = run(probe)
+    rows = int(min(T, max(probe, probe * target_s / max(dt, 1e-6))))
+    dt = run(rows)
+    return {"value": rows / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"first {rows} of {T} rows of the same inputs, {dt:.2f} s, "
+                      f"OpenMP over rows ({threads} threads)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target duration of the CPU-baseline sample (0 disables it)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); MhcPre shards "
+              "over rows with no exchange, so N GPUs run N independent copies.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from __graft_entry__ import load_package
+
+    pkg = load_package()
+    pkg.load_library()
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+    n, D, T, bf16, gamma_on, _ = WORKLOADS[args.config]
+    x, phi, alpha, bias, gamma = make_inputs(args.config, device)
+    op = pkg.MhcPreOp(x, phi, alpha, bias, gamma)
+    stream = torch.cuda.current_stream()
+
+    for _ in range(args.warmup):
+        op.launch(stream)
+    torch.cuda.synchronize()
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        op.launch(stream)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    durs = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))  # ms per launch
+    total_ms = starts[0].elapsed_time(ends[-1])
+    mean_ms = sum(durs) / len(durs)
+    status = op.device_status(stream)
+    if status != 0:
+        print(f"device status {status}", file=sys.stderr)
+        return 1
+
+    b_alg = algorithmic_bytes(n, D, T, bf16, gamma_on)
+    achieved = b_alg / (mean_ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": T / (mean_ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": total_ms / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if bf16 else "fp16",
+        "data": "synthetic",
+        "config": {"workload": f"mhc_pre n={n} D={D} T={T} {'bf16' if bf16 else 'fp16'} "
+                               f"gamma={'on' if gamma_on else 'off'}",
+                   "n": n, "D": D, "T": T, "gamma": gamma_on, "path": op.path,
+                   "median_us": durs[len(durs) // 2] * 1e3, "min_us": durs[0] * 1e3,
+                   "algorithmic_bytes": b_alg},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+    }
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_baseline(x, phi, alpha, bias, gamma, bf16,
+                                              args.cpu_seconds)
+    op.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

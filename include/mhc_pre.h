@@ -1,0 +1,147 @@
+/*
+ * MhcPre for AMD Instinct MI355X (gfx950): C ABI.
+ *
+ * MhcPre is the pre-mixing step of a multi-stream (hyper-connection) residual
+ * block.  For every token row r of x [T, n, D] (T = B*S, K = n*D,
+ * M = n*n + 2n):
+ *
+ *   invRms  = 1 / sqrt(sum_k x[r,k]^2 / K + normEps)
+ *   mix[j]  = sum_k (x[r,k] * gamma[k]) * phi_mem[j*K + k]          (j < M)
+ *   hPre[i] = sigmoid(mix[i]     * (invRms*alpha[0]) + bias[i])     + hcEps
+ *   hPost[i]= 2 * sigmoid(mix[n+i] * (invRms*alpha[1]) + bias[n+i])
+ *   hRes[i*n+j] = mix[2n+i*n+j] * (invRms*alpha[2]) + bias[2n+i*n+j]
+ *   hIn[r,d]= RNE_dtype(sum_s hPre[s] * x[r,s,d])
+ *
+ * The API mirrors the reference operator's generated two-phase aclnn API
+ * (aclnnMhcPreGetWorkspaceSize / aclnnMhcPre, as called at
+ * cloud_runner/runner.cpp:443-445,459): phase 1 validates the tensors, sizes
+ * the device workspace and returns an executor bound to the tensors' device
+ * addresses; phase 2 launches on a HIP stream.  The caller owns every device
+ * buffer, including the workspace.  The executor is immutable after creation:
+ * it may be launched any number of times (the reference probe relaunches one
+ * executor, cloud_runner/probe_e1e2.cpp:312-326) and from several host threads
+ * on different streams, provided the launches do not share a workspace
+ * concurrently.  No function aborts; every failure is a status code.
+ */
+#ifndef MHC_PRE_H
+#define MHC_PRE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Exported symbols (the library is built with hidden default visibility). */
+#ifndef MHC_API
+#define MHC_API __attribute__((visibility("default")))
+#endif
+
+/* Same declaration as HIP's runtime header, so callers need no HIP include. */
+typedef struct ihipStream_t *hipStream_t;
+
+/* Element types.  The values are those of the reference stack's aclDataType
+ * (ACL_FLOAT = 0, ACL_FLOAT16 = 1, ACL_BF16 = 27) so a binding can pass them
+ * through unchanged. */
+#define MHC_DTYPE_FLOAT 0
+#define MHC_DTYPE_FLOAT16 1
+#define MHC_DTYPE_BF16 27
+
+#define MHC_MAX_DIMS 8
+
+/* A dense row-major tensor over caller-owned device memory (aclTensor's role,
+ * cloud_runner/runner.cpp:217-218).  `data` may be NULL only for an absent
+ * optional tensor or one with zero elements. */
+typedef struct mhcTensor {
+    void *data;
+    int32_t dtype;
+    int32_t ndim;
+    int64_t dims[MHC_MAX_DIMS];
+} mhcTensor;
+
+typedef struct mhcPreExecutor mhcPreExecutor;
+
+/* Status codes (0 = success, like ACL_SUCCESS). */
+#define MHC_STATUS_SUCCESS 0
+#define MHC_STATUS_NULL_ARGUMENT 1        /* a required pointer is NULL */
+#define MHC_STATUS_INVALID_SHAPE 2        /* rank / dims / element counts inconsistent */
+#define MHC_STATUS_UNSUPPORTED_SHAPE 3    /* n not in {4,6,8}, D % 16, n*D % 8, M > 80 */
+#define MHC_STATUS_INVALID_DTYPE 4        /* x not fp16/bf16, fp32 tensors not fp32, hIn != x */
+#define MHC_STATUS_WORKSPACE_TOO_SMALL 5  /* workspace NULL or smaller than phase 1 asked */
+#define MHC_STATUS_HIP_ERROR 6            /* a HIP runtime call failed */
+#define MHC_STATUS_DEVICE_MISMATCH 7      /* launched on a device the executor cannot run on */
+#define MHC_STATUS_DEVICE_TIMEOUT 8       /* a kernel's bounded inter-workgroup wait expired */
+#define MHC_STATUS_MISALIGNED 9           /* x, hIn, phi, gamma not 16-byte aligned; others not 4 */
+
+/*
+ * Phase 1.  Replaces aclnnMhcPreGetWorkspaceSize (argument list and meaning
+ * as cloud_runner/runner.cpp:443-445; validation rules of the reference
+ * TilingFunc, code/op_host/mhc_pre.cpp:57-79,126-130; output shapes of its
+ * InferShape / InferDataType, code/op_host/mhc_pre.cpp:217-257).
+ *
+ *   x      fp16 | bf16  [B, S, n, D]  (a 3-D [T, n, D] is accepted as an extension)
+ *   phi    fp32         n*D*M elements, read as memory [M][K] (phi_mem[j*K + k])
+ *   alpha  fp32         3 elements {alphaPre, alphaPost, alphaRes}
+ *   bias   fp32         M elements: [0,n) pre, [n,2n) post, [2n, 2n+n*n) res
+ *   gamma  fp32         n*D elements, or NULL / zero elements => gamma off
+ *                       (code/op_host/mhc_pre.cpp:90)
+ *   normEps, hcEps      the op attributes (reference defaults 1e-6,
+ *                       code/op_host/mhc_pre.cpp:297-298)
+ *   hIn    dtype of x   [B, S, D]
+ *   hPost  fp32         [B, S, n]
+ *   hRes   fp32         [B, S, n, n]
+ * On success *workspaceSize holds the bytes the caller must allocate and
+ * *executor a new executor (free it with mhcPreExecutorDestroy).
+ */
+MHC_API int mhcPreGetWorkspaceSize(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alpha,
+                           const mhcTensor *bias, const mhcTensor *gamma, float normEps,
+                           float hcEps, const mhcTensor *hIn, const mhcTensor *hPost,
+                           const mhcTensor *hRes, uint64_t *workspaceSize,
+                           mhcPreExecutor **executor);
+
+/*
+ * Phase 1 with one extra optional output, hPre fp32 [B, S, n] (NULL => not
+ * written).  Extension: the reference keeps hPre on chip only
+ * (code/op_kernel/mhc_pre.cpp:742-750); everything else is as
+ * mhcPreGetWorkspaceSize.
+ */
+MHC_API int mhcPreGetWorkspaceSizeWithHPre(const mhcTensor *x, const mhcTensor *phi,
+                                   const mhcTensor *alpha, const mhcTensor *bias,
+                                   const mhcTensor *gamma, float normEps, float hcEps,
+                                   const mhcTensor *hIn, const mhcTensor *hPost,
+                                   const mhcTensor *hRes, const mhcTensor *hPre,
+                                   uint64_t *workspaceSize, mhcPreExecutor **executor);
+
+/*
+ * Phase 2.  Replaces aclnnMhcPre (cloud_runner/runner.cpp:459,472): enqueues
+ * the operator on `stream` (NULL = the null stream) and returns without
+ * waiting.  The workspace must hold at least the bytes phase 1 returned.
+ */
+MHC_API int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor,
+           hipStream_t stream);
+
+/* Releases an executor (the generated aclnn API frees executors itself). */
+MHC_API int mhcPreExecutorDestroy(mhcPreExecutor *executor);
+
+/*
+ * Device-side status of the last completed launch that used `workspace`:
+ * MHC_STATUS_SUCCESS, or MHC_STATUS_DEVICE_TIMEOUT if a bounded wait between
+ * workgroups expired.  Synchronizes `stream` first.  No reference counterpart
+ * (the reference detects a hang only by the caller's own wait,
+ * cloud_runner/probe_e1e2.cpp:295).
+ */
+MHC_API int mhcPreQueryDeviceStatus(void *workspace, uint64_t workspaceSize,
+                            const mhcPreExecutor *executor, hipStream_t stream);
+
+/* Human-readable name of a status code (static storage). */
+MHC_API const char *mhcPreStatusString(int status);
+
+/* Which kernel path an executor launches (diagnostics and benchmarks):
+ * writes a static NUL-terminated name to *name. */
+MHC_API int mhcPreExecutorPath(const mhcPreExecutor *executor, const char **name);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MHC_PRE_H */

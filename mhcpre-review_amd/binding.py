@@ -1,0 +1,242 @@
+"""ctypes binding of ``include/mhc_pre.h`` (libmhcpre.so).
+
+Mirrors the reference's two-phase aclnn usage (cloud_runner/runner.cpp:440-476):
+phase 1 ``mhcPreGetWorkspaceSize`` validates and returns (workspace bytes,
+executor); phase 2 ``mhcPre`` launches on a stream.  PyTorch supplies device
+memory and the stream handle only.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from pathlib import Path
+from typing import Optional, Sequence
+
+MHC_DTYPE_FLOAT = 0
+MHC_DTYPE_FLOAT16 = 1
+MHC_DTYPE_BF16 = 27
+MHC_MAX_DIMS = 8
+
+STATUS = {
+    0: "MHC_STATUS_SUCCESS",
+    1: "MHC_STATUS_NULL_ARGUMENT",
+    2: "MHC_STATUS_INVALID_SHAPE",
+    3: "MHC_STATUS_UNSUPPORTED_SHAPE",
+    4: "MHC_STATUS_INVALID_DTYPE",
+    5: "MHC_STATUS_WORKSPACE_TOO_SMALL",
+    6: "MHC_STATUS_HIP_ERROR",
+    7: "MHC_STATUS_DEVICE_MISMATCH",
+    8: "MHC_STATUS_DEVICE_TIMEOUT",
+    9: "MHC_STATUS_MISALIGNED",
+}
+STATUS_CODE = {v: k for k, v in STATUS.items()}
+
+_PKG_DIR = Path(__file__).resolve().parent
+_REPO_DIR = _PKG_DIR.parent
+HEADER = _REPO_DIR / "include" / "mhc_pre.h"
+
+
+class MhcTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("dims", ctypes.c_int64 * MHC_MAX_DIMS),
+    ]
+
+
+class MhcPreError(RuntimeError):
+    def __init__(self, where: str, status: int):
+        super().__init__(f"{where} failed: {STATUS.get(status, status)} ({status})")
+        self.status = status
+
+
+def library_path() -> Path:
+    return Path(os.environ.get("MHCPRE_LIB", _PKG_DIR / "libmhcpre.so"))
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Load libmhcpre.so.  Raises if it is absent: there is no fallback path."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not path.exists():
+        raise FileNotFoundError(
+            f"{path} not built; build it with `make -C mhcpre-review_amd/csrc` "
+            "or __graft_entry__.build()")
+    lib = ctypes.CDLL(str(path))
+    P = ctypes.POINTER
+    T = P(MhcTensor)
+    exe = ctypes.c_void_p
+    lib.mhcPreGetWorkspaceSize.argtypes = [T, T, T, T, T, ctypes.c_float, ctypes.c_float,
+                                           T, T, T, P(ctypes.c_uint64), P(exe)]
+    lib.mhcPreGetWorkspaceSize.restype = ctypes.c_int
+    lib.mhcPreGetWorkspaceSizeWithHPre.argtypes = [T, T, T, T, T, ctypes.c_float,
+                                                   ctypes.c_float, T, T, T, T,
+                                                   P(ctypes.c_uint64), P(exe)]
+    lib.mhcPreGetWorkspaceSizeWithHPre.restype = ctypes.c_int
+    lib.mhcPre.argtypes = [ctypes.c_void_p, ctypes.c_uint64, exe, ctypes.c_void_p]
+    lib.mhcPre.restype = ctypes.c_int
+    lib.mhcPreExecutorDestroy.argtypes = [exe]
+    lib.mhcPreExecutorDestroy.restype = ctypes.c_int
+    lib.mhcPreQueryDeviceStatus.argtypes = [ctypes.c_void_p, ctypes.c_uint64, exe,
+                                            ctypes.c_void_p]
+    lib.mhcPreQueryDeviceStatus.restype = ctypes.c_int
+    lib.mhcPreStatusString.argtypes = [ctypes.c_int]
+    lib.mhcPreStatusString.restype = ctypes.c_char_p
+    lib.mhcPreExecutorPath.argtypes = [exe, P(ctypes.c_char_p)]
+    lib.mhcPreExecutorPath.restype = ctypes.c_int
+    _LIB = lib
+    return lib
+
+
+def exported_symbols(header: Path = HEADER) -> list[str]:
+    """Names of the functions the public header declares (MHC_API ...)."""
+    text = header.read_text()
+    return re.findall(r"^MHC_API\s+[\w\s\*]*?\b(\w+)\s*\(", text, flags=re.MULTILINE)
+
+
+def make_tensor(data_ptr: int, dtype: int, dims: Sequence[int]) -> MhcTensor:
+    t = MhcTensor()
+    t.data = ctypes.c_void_p(int(data_ptr)) if data_ptr else None
+    t.dtype = int(dtype)
+    t.ndim = len(dims)
+    if t.ndim > MHC_MAX_DIMS:
+        raise ValueError("too many dims")
+    for i, d in enumerate(dims):
+        t.dims[i] = int(d)
+    return t
+
+
+def _torch_dtype_code(dt) -> int:
+    import torch
+
+    return {torch.float32: MHC_DTYPE_FLOAT, torch.float16: MHC_DTYPE_FLOAT16,
+            torch.bfloat16: MHC_DTYPE_BF16}[dt]
+
+
+def tensor_desc(t, dims: Optional[Sequence[int]] = None) -> MhcTensor:
+    """Descriptor over a torch tensor's device memory (must be contiguous)."""
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return make_tensor(t.data_ptr(), _torch_dtype_code(t.dtype),
+                       list(t.shape) if dims is None else list(dims))
+
+
+def _stream_handle(stream) -> int:
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return int(stream.cuda_stream)
+
+
+class MhcPreOp:
+    """One executor plus its workspace: phase 1 at construction, phase 2 per launch.
+
+    Outputs not given are allocated on x's device.  ``h_pre=True`` allocates the
+    optional hPre output (extension entry point).  phi is passed with its
+    declared shape [n*D, M] unless ``phi_dims`` overrides it; its memory is
+    read as [M][K] either way.
+    """
+
+    def __init__(self, x, phi, alpha, bias, gamma=None, norm_eps: float = 1e-6,
+                 hc_eps: float = 1e-6, h_in=None, h_post=None, h_res=None, h_pre=None,
+                 phi_dims=None):
+        import torch
+
+        self.lib = load_library()
+        lead = list(x.shape[:-2])
+        n, D = int(x.shape[-2]), int(x.shape[-1])
+        dev = x.device
+        self.h_in = h_in if h_in is not None else torch.empty(lead + [D], dtype=x.dtype,
+                                                               device=dev)
+        self.h_post = h_post if h_post is not None else torch.empty(lead + [n],
+                                                                    dtype=torch.float32,
+                                                                    device=dev)
+        self.h_res = h_res if h_res is not None else torch.empty(lead + [n, n],
+                                                                 dtype=torch.float32,
+                                                                 device=dev)
+        if h_pre is True:
+            h_pre = torch.empty(lead + [n], dtype=torch.float32, device=dev)
+        self.h_pre = h_pre if h_pre is not False else None
+        # Keep the inputs alive as long as the executor that binds them.
+        self._keep = (x, phi, alpha, bias, gamma)
+        descs = [tensor_desc(x), tensor_desc(phi, phi_dims), tensor_desc(alpha),
+                 tensor_desc(bias)]
+        g = tensor_desc(gamma) if gamma is not None else None
+        outs = [tensor_desc(self.h_in), tensor_desc(self.h_post), tensor_desc(self.h_res)]
+        ws = ctypes.c_uint64(0)
+        exe = ctypes.c_void_p(None)
+        gp = ctypes.byref(g) if g is not None else None
+        if self.h_pre is not None:
+            hp = tensor_desc(self.h_pre)
+            st = self.lib.mhcPreGetWorkspaceSizeWithHPre(
+                *[ctypes.byref(d) for d in descs], gp, ctypes.c_float(norm_eps),
+                ctypes.c_float(hc_eps), *[ctypes.byref(d) for d in outs], ctypes.byref(hp),
+                ctypes.byref(ws), ctypes.byref(exe))
+        else:
+            st = self.lib.mhcPreGetWorkspaceSize(
+                *[ctypes.byref(d) for d in descs], gp, ctypes.c_float(norm_eps),
+                ctypes.c_float(hc_eps), *[ctypes.byref(d) for d in outs], ctypes.byref(ws),
+                ctypes.byref(exe))
+        if st != 0:
+            raise MhcPreError("mhcPreGetWorkspaceSize", st)
+        self.executor = exe
+        self.workspace_size = int(ws.value)
+        self.workspace = torch.empty(max(self.workspace_size, 256), dtype=torch.uint8,
+                                     device=dev)
+
+    @property
+    def path(self) -> str:
+        name = ctypes.c_char_p()
+        st = self.lib.mhcPreExecutorPath(self.executor, ctypes.byref(name))
+        if st != 0:
+            raise MhcPreError("mhcPreExecutorPath", st)
+        return name.value.decode()
+
+    def launch(self, stream=None) -> None:
+        st = self.lib.mhcPre(ctypes.c_void_p(self.workspace.data_ptr()),
+                             ctypes.c_uint64(self.workspace_size), self.executor,
+                             ctypes.c_void_p(_stream_handle(stream)))
+        if st != 0:
+            raise MhcPreError("mhcPre", st)
+
+    def device_status(self, stream=None) -> int:
+        return self.lib.mhcPreQueryDeviceStatus(ctypes.c_void_p(self.workspace.data_ptr()),
+                                                ctypes.c_uint64(self.workspace_size),
+                                                self.executor,
+                                                ctypes.c_void_p(_stream_handle(stream)))
+
+    def close(self) -> None:
+        if getattr(self, "executor", None) is not None and self.executor.value:
+            self.lib.mhcPreExecutorDestroy(self.executor)
+            self.executor = ctypes.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def outputs(self):
+        return self.h_in, self.h_post, self.h_res, self.h_pre
+
+
+def mhc_pre(x, phi, alpha, bias, gamma=None, norm_eps: float = 1e-6, hc_eps: float = 1e-6,
+            h_pre: bool = False, stream=None):
+    """One call: returns (hIn, hPost, hRes, hPre-or-None) after the launch is enqueued."""
+    op = MhcPreOp(x, phi, alpha, bias, gamma, norm_eps, hc_eps, h_pre=True if h_pre else None)
+    op.launch(stream)
+    # The workspace must outlive the launch: hold it until the stream is idle.
+    import torch
+
+    torch.cuda.current_stream().synchronize() if stream is None else stream.synchronize()
+    outs = op.outputs()
+    op.close()
+    return outs

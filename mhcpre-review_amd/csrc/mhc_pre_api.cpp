@@ -1,0 +1,344 @@
+// MhcPre host library: validation, launch plan, workspace sizing and launch.
+//
+// Mirrors the reference host op (code/op_host/mhc_pre.cpp): the acceptance
+// rules of TilingFunc (:57-79,126-130), the output shapes and types of
+// InferShape / InferDataType (:217-257), the attribute defaults (:297-298) and
+// the gamma-presence rule (:90).  The Ascend tiling (row partition over 48 AIV
+// cores, Cube M64 tiling, UB budgeting) has no counterpart: the GPU plan is a
+// grid shape and a workspace layout.  Unlike the reference's process-global
+// tiling cache (:36-51,99-121), nothing here is shared between calls, so
+// concurrent phase-1 calls are safe.
+
+#include "mhc_pre.h"
+#include "mhc_pre_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <new>
+
+struct mhcPreExecutor {
+    mhc::Plan plan;
+    int device = -1;  // device the executor was planned on (-1: none visible at plan time)
+};
+
+namespace {
+
+int64_t numel(const mhcTensor &t)
+{
+    int64_t n = 1;
+    for (int i = 0; i < t.ndim; ++i) {
+        n *= t.dims[i];
+    }
+    return n;
+}
+
+bool dims_positive(const mhcTensor &t)
+{
+    if (t.ndim < 0 || t.ndim > MHC_MAX_DIMS) {
+        return false;
+    }
+    for (int i = 0; i < t.ndim; ++i) {
+        if (t.dims[i] <= 0) {
+            return false;
+        }
+    }
+    return true;
+}
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Trailing dims of `t` must be `tail` and its element count `count`.
+bool shape_matches(const mhcTensor &t, int64_t count, const int64_t *tail, int ntail)
+{
+    if (!dims_positive(t) || t.ndim < ntail || numel(t) != count) {
+        return false;
+    }
+    for (int i = 0; i < ntail; ++i) {
+        if (t.dims[t.ndim - ntail + i] != tail[i]) {
+            return false;
+        }
+    }
+    return true;
+}
+
+int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alpha,
+                      const mhcTensor *bias, const mhcTensor *gamma, float normEps, float hcEps,
+                      const mhcTensor *hIn, const mhcTensor *hPost, const mhcTensor *hRes,
+                      const mhcTensor *hPre, mhc::Plan &p)
+{
+    if (x == nullptr || phi == nullptr || alpha == nullptr || bias == nullptr || hIn == nullptr ||
+        hPost == nullptr || hRes == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    // x must be 4-D [B, S, n, D] (code/op_host/mhc_pre.cpp:67-70); 3-D [T, n, D]
+    // is accepted as an extension.
+    if (x->ndim != 4 && x->ndim != 3) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    int64_t T = 1;
+    for (int i = 0; i + 2 < x->ndim; ++i) {
+        if (x->dims[i] <= 0) {
+            return MHC_STATUS_INVALID_SHAPE;
+        }
+        T *= x->dims[i];
+    }
+    const int64_t n64 = x->dims[x->ndim - 2];
+    const int64_t D = x->dims[x->ndim - 1];
+    if (D <= 0) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    // Supported stream counts and alignments (code/op_host/mhc_pre.cpp:76-79,126-128).
+    if (n64 != 4 && n64 != 6 && n64 != 8) {
+        return MHC_STATUS_UNSUPPORTED_SHAPE;
+    }
+    const int n = static_cast<int>(n64);
+    const int64_t K = n64 * D;
+    const int M = n * n + 2 * n;
+    if (M > 80 || (K % 8) != 0 || (D % 16) != 0) {
+        return MHC_STATUS_UNSUPPORTED_SHAPE;
+    }
+
+    // Types (code/op_host/mhc_pre.cpp:265-296; InferDataType :251-257).
+    if (x->dtype != MHC_DTYPE_FLOAT16 && x->dtype != MHC_DTYPE_BF16) {
+        return MHC_STATUS_INVALID_DTYPE;
+    }
+    const bool hasGamma = gamma != nullptr && numel(*gamma) > 0 && gamma->ndim > 0;
+    if (phi->dtype != MHC_DTYPE_FLOAT || alpha->dtype != MHC_DTYPE_FLOAT ||
+        bias->dtype != MHC_DTYPE_FLOAT || hPost->dtype != MHC_DTYPE_FLOAT ||
+        hRes->dtype != MHC_DTYPE_FLOAT || hIn->dtype != x->dtype ||
+        (hasGamma && gamma->dtype != MHC_DTYPE_FLOAT) ||
+        (hPre != nullptr && hPre->dtype != MHC_DTYPE_FLOAT)) {
+        return MHC_STATUS_INVALID_DTYPE;
+    }
+
+    // Element counts.  The reference never checks these (only x is
+    // shape-checked); reading past a short phi would be silent there.
+    if (!dims_positive(*phi) || numel(*phi) != K * M || !dims_positive(*alpha) ||
+        numel(*alpha) != 3 || !dims_positive(*bias) || numel(*bias) != M) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    if (hasGamma && (!dims_positive(*gamma) || numel(*gamma) != K)) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    // Output shapes as InferShape: hIn [.., D], hPost [.., n], hRes [.., n, n].
+    const int64_t tailD[1] = {D};
+    const int64_t tailN[1] = {n64};
+    const int64_t tailNN[2] = {n64, n64};
+    if (!shape_matches(*hIn, T * D, tailD, 1) || !shape_matches(*hPost, T * n64, tailN, 1) ||
+        !shape_matches(*hRes, T * n64 * n64, tailNN, 2) ||
+        (hPre != nullptr && !shape_matches(*hPre, T * n64, tailN, 1))) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+
+    // Device addresses.
+    if (x->data == nullptr || phi->data == nullptr || alpha->data == nullptr ||
+        bias->data == nullptr || hIn->data == nullptr || hPost->data == nullptr ||
+        hRes->data == nullptr || (hasGamma && gamma->data == nullptr) ||
+        (hPre != nullptr && hPre->data == nullptr)) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    if (!aligned(x->data, 16) || !aligned(hIn->data, 16) || !aligned(phi->data, 16) ||
+        (hasGamma && !aligned(gamma->data, 16)) || !aligned(alpha->data, 4) ||
+        !aligned(bias->data, 4) || !aligned(hPost->data, 4) || !aligned(hRes->data, 4) ||
+        (hPre != nullptr && !aligned(hPre->data, 4))) {
+        return MHC_STATUS_MISALIGNED;
+    }
+
+    p = mhc::Plan{};
+    p.n = n;
+    p.M = M;
+    p.NT = (2 * M) / 16;
+    p.T = T;
+    p.D = D;
+    p.K = K;
+    p.isBf16 = x->dtype == MHC_DTYPE_BF16;
+    p.hasGamma = hasGamma;
+    p.hasHPre = hPre != nullptr;
+    p.normEps = normEps;
+    p.hcEps = hcEps;
+    p.invFlatDim = 1.0f / static_cast<float>(K);
+    p.x = x->data;
+    p.phi = static_cast<const float *>(phi->data);
+    p.alpha = static_cast<const float *>(alpha->data);
+    p.bias = static_cast<const float *>(bias->data);
+    p.gamma = hasGamma ? static_cast<const float *>(gamma->data) : nullptr;
+    p.hIn = hIn->data;
+    p.hPost = static_cast<float *>(hPost->data);
+    p.hRes = static_cast<float *>(hRes->data);
+    p.hPre = hPre != nullptr ? static_cast<float *>(hPre->data) : nullptr;
+
+    // Split path plan: enough (row tile, K-slice) workgroups to fill the chip,
+    // at least 16 k-steps (4 per wave) per slice.  Shape-only, so the
+    // workspace size does not depend on the device.
+    const int64_t rowTiles = (T + 15) / 16;
+    const int64_t ksTotal = K / 32;
+    const int64_t maxSlices = std::max<int64_t>(1, ksTotal / 16);
+    int64_t S = std::min<int64_t>(maxSlices, std::max<int64_t>(1, (2048 + rowTiles - 1) / rowTiles));
+    const int64_t ksPer = (ksTotal + S - 1) / S;
+    S = (ksTotal + ksPer - 1) / ksPer;
+    p.splitS = static_cast<int>(S);
+    p.ksPerSlice = static_cast<int>(ksPer);
+    p.path = mhc::Path::kSplit;
+
+    size_t off = mhc::kWsHeaderBytes;
+    p.wsBsplit = off;
+    off = align_up(off + static_cast<size_t>(K) * static_cast<size_t>(2 * M) * 2, 256);
+    p.wsPartial = off;
+    off = align_up(off + static_cast<size_t>(S) * static_cast<size_t>(T) * (M + 1) * 4, 256);
+    p.wsCounters = off;
+    p.wsTotal = off;
+    return MHC_STATUS_SUCCESS;
+}
+
+int get_workspace(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alpha,
+                  const mhcTensor *bias, const mhcTensor *gamma, float normEps, float hcEps,
+                  const mhcTensor *hIn, const mhcTensor *hPost, const mhcTensor *hRes,
+                  const mhcTensor *hPre, uint64_t *workspaceSize, mhcPreExecutor **executor)
+{
+    if (workspaceSize == nullptr || executor == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    *executor = nullptr;
+    mhc::Plan plan;
+    const int st = validate_and_plan(x, phi, alpha, bias, gamma, normEps, hcEps, hIn, hPost, hRes, hPre,
+                               plan);
+    if (st != MHC_STATUS_SUCCESS) {
+        return st;
+    }
+    mhcPreExecutor *ex = new (std::nothrow) mhcPreExecutor;
+    if (ex == nullptr) {
+        return MHC_STATUS_HIP_ERROR;
+    }
+    ex->plan = plan;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        dev = -1;
+    }
+    ex->device = dev;
+    *workspaceSize = plan.wsTotal;
+    *executor = ex;
+    return MHC_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mhcPreGetWorkspaceSize(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alpha,
+                           const mhcTensor *bias, const mhcTensor *gamma, float normEps,
+                           float hcEps, const mhcTensor *hIn, const mhcTensor *hPost,
+                           const mhcTensor *hRes, uint64_t *workspaceSize,
+                           mhcPreExecutor **executor)
+{
+    return get_workspace(x, phi, alpha, bias, gamma, normEps, hcEps, hIn, hPost, hRes, nullptr,
+                         workspaceSize, executor);
+}
+
+int mhcPreGetWorkspaceSizeWithHPre(const mhcTensor *x, const mhcTensor *phi,
+                                   const mhcTensor *alpha, const mhcTensor *bias,
+                                   const mhcTensor *gamma, float normEps, float hcEps,
+                                   const mhcTensor *hIn, const mhcTensor *hPost,
+                                   const mhcTensor *hRes, const mhcTensor *hPre,
+                                   uint64_t *workspaceSize, mhcPreExecutor **executor)
+{
+    return get_workspace(x, phi, alpha, bias, gamma, normEps, hcEps, hIn, hPost, hRes, hPre,
+                         workspaceSize, executor);
+}
+
+int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hipStream_t stream)
+{
+    if (executor == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    const mhc::Plan &p = executor->plan;
+    if (workspace == nullptr || workspaceSize < p.wsTotal) {
+        return MHC_STATUS_WORKSPACE_TOO_SMALL;
+    }
+    if (!aligned(workspace, 256)) {
+        return MHC_STATUS_WORKSPACE_TOO_SMALL;
+    }
+    hipError_t err;
+    switch (p.path) {
+    case mhc::Path::kFused:
+        err = mhc::launch_fused(p, workspace, stream);
+        break;
+    case mhc::Path::kSplit:
+    default:
+        err = mhc::launch_split(p, workspace, stream);
+        break;
+    }
+    return err == hipSuccess ? MHC_STATUS_SUCCESS : MHC_STATUS_HIP_ERROR;
+}
+
+int mhcPreExecutorDestroy(mhcPreExecutor *executor)
+{
+    if (executor == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    delete executor;
+    return MHC_STATUS_SUCCESS;
+}
+
+int mhcPreQueryDeviceStatus(void *workspace, uint64_t workspaceSize,
+                            const mhcPreExecutor *executor, hipStream_t stream)
+{
+    if (executor == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    if (workspace == nullptr || workspaceSize < executor->plan.wsTotal) {
+        return MHC_STATUS_WORKSPACE_TOO_SMALL;
+    }
+    if (hipStreamSynchronize(stream) != hipSuccess) {
+        return MHC_STATUS_HIP_ERROR;
+    }
+    uint32_t word = 0;
+    if (hipMemcpy(&word, workspace, sizeof(word), hipMemcpyDeviceToHost) != hipSuccess) {
+        return MHC_STATUS_HIP_ERROR;
+    }
+    return word == mhc::kDeviceOk ? MHC_STATUS_SUCCESS : MHC_STATUS_DEVICE_TIMEOUT;
+}
+
+const char *mhcPreStatusString(int status)
+{
+    switch (status) {
+    case MHC_STATUS_SUCCESS:
+        return "success";
+    case MHC_STATUS_NULL_ARGUMENT:
+        return "null argument";
+    case MHC_STATUS_INVALID_SHAPE:
+        return "invalid shape";
+    case MHC_STATUS_UNSUPPORTED_SHAPE:
+        return "unsupported shape";
+    case MHC_STATUS_INVALID_DTYPE:
+        return "invalid dtype";
+    case MHC_STATUS_WORKSPACE_TOO_SMALL:
+        return "workspace too small";
+    case MHC_STATUS_HIP_ERROR:
+        return "HIP error";
+    case MHC_STATUS_DEVICE_MISMATCH:
+        return "device mismatch";
+    case MHC_STATUS_DEVICE_TIMEOUT:
+        return "device timeout";
+    case MHC_STATUS_MISALIGNED:
+        return "misaligned device pointer";
+    default:
+        return "unknown status";
+    }
+}
+
+int mhcPreExecutorPath(const mhcPreExecutor *executor, const char **name)
+{
+    if (executor == nullptr || name == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    *name = executor->plan.path == mhc::Path::kFused ? "fused" : "split";
+    return MHC_STATUS_SUCCESS;
+}
+
+}  // extern "C"

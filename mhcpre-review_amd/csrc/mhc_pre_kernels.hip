@@ -1,0 +1,435 @@
+// MhcPre HIP kernels for gfx950 (CDNA4).
+//
+// Stages (reference: code/op_kernel/mhc_pre.cpp):
+//   prep_b          gamma (.) phi split into bf16 hi + lo, laid out as MFMA B fragments
+//   gemm_partial    split-K mixing GEMM on bf16 MFMA (fp32 accumulate) + sum of squares
+//   epilogue_hin    fixed-order reduction of the partials, invRms, sigmoid / affine
+//                   epilogue, weighted stream reduction with RNE stores
+//
+// Numerics.  x (bf16) is exact as an MFMA operand; fp16 x is split exactly into
+// bf16 hi + lo.  B = gamma*phi (fp32) is split into bf16 hi + lo with a residual
+// below 2^-17 |B|, and both halves go through the MFMA into fp32 accumulators,
+// so the GEMM carries fp32-level accuracy at bf16 MFMA rate.  Everything after
+// the GEMM is fp32 in the reference kernel's operation order (built with
+// -ffp-contract=off: one rounding per product and per sum).
+
+#include "mhc_pre_internal.h"
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mhc {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+template <int N>
+struct Shape {
+    static constexpr int M = N * N + 2 * N;     // mix columns
+    static constexpr int NT = (2 * M) / 16;     // [hi | lo] column tiles
+    static constexpr int NTHI = (M + 15) / 16;  // tiles holding a hi column
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// Round-half-even conversions (v_cvt_pk_bf16_f32 / v_cvt_f16_f32).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
+{
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f)
+{
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+template <bool kBf16>
+__device__ __forceinline__ float x_to_f32(uint32_t bits)
+{
+    return kBf16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+}
+
+template <bool kBf16>
+__device__ __forceinline__ uint32_t f32_to_x(float f)
+{
+    return kBf16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f);
+}
+
+// Unpack 8 16-bit values held in a u32x4 (element e in half e&1 of word e>>1).
+template <bool kBf16>
+__device__ __forceinline__ void unpack8(const u32x4_t &v, float (&f)[8])
+{
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        f[2 * w] = x_to_f32<kBf16>(v[w] & 0xFFFFu);
+        f[2 * w + 1] = x_to_f32<kBf16>(v[w] >> 16);
+    }
+}
+
+__device__ __forceinline__ u32x4_t pack8_bf16(const float (&f)[8])
+{
+    u32x4_t r;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        r[w] = f32_to_bf16_bits(f[2 * w]) | (f32_to_bf16_bits(f[2 * w + 1]) << 16);
+    }
+    return r;
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t &v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ f32x4_t mfma16(const u32x4_t &a, const u32x4_t &b, const f32x4_t &c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// fp16 x -> exact bf16 pair: x = hi + lo (an fp16 significand has 11 bits).
+__device__ __forceinline__ void split_f16_to_bf16(const float (&f)[8], u32x4_t &hi, u32x4_t &lo)
+{
+    float h[8], l[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        h[e] = bf16_bits_to_f32(f32_to_bf16_bits(f[e]));
+        l[e] = f[e] - h[e];
+    }
+    hi = pack8_bf16(h);
+    lo = pack8_bf16(l);
+}
+
+// Sigmoid in the reference vector order (code/op_kernel/mhc_pre.cpp:542-555):
+// scale, +bias, negate, exp, +1, reciprocal, +eps (only when eps != 0).
+__device__ __forceinline__ float ref_sigmoid(float scaled, float bias, float eps)
+{
+    float v = scaled + bias;
+    v = -v;
+    v = expf(v);
+    v = v + 1.0f;
+    v = 1.0f / v;
+    if (eps != 0.0f) {
+        v = v + eps;
+    }
+    return v;
+}
+
+// invRms = 1 / sqrt(sumsq * invFlatDim + normEps) (code/op_kernel/mhc_pre.cpp:504-519).
+__device__ __forceinline__ float ref_inv_rms(float sumsq, float invFlatDim, float normEps)
+{
+    float v = sumsq * invFlatDim;
+    v = v + normEps;
+    v = sqrtf(v);
+    return 1.0f / v;
+}
+
+// ---------------------------------------------------------------------------
+// prep_b: B operand fragments.
+//
+// Layout: [ks = K/32][ct = NT][lane 64] x 16 bytes.  Lane l of fragment
+// (ks, ct) holds B[k = 32ks + 8(l/16) + e][c = 16ct + l%16] for e = 0..7,
+// where column c < M is hi(gamma[k]*phi_mem[c*K + k]) and c >= M is the lo
+// half of column c - M.  A wave loads one fragment as 1 KiB contiguous.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prep_b_kernel(const float *__restrict__ phi,
+                                                     const float *__restrict__ gamma,
+                                                     u32x4_t *__restrict__ bsplit, int64_t K,
+                                                     int M, int NT, uint32_t *__restrict__ status)
+{
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx == 0 && status != nullptr) {
+        *status = kDeviceOk;
+    }
+    const int64_t total = (K / 32) * NT * kWave;
+    if (idx >= total) {
+        return;
+    }
+    const int lane = (int)(idx % kWave);
+    const int ct = (int)((idx / kWave) % NT);
+    const int64_t ks = idx / ((int64_t)kWave * NT);
+    const int c = 16 * ct + (lane & 15);
+    const bool isLo = c >= M;
+    const int j = isLo ? c - M : c;
+    const int64_t k0 = ks * 32 + 8 * (lane >> 4);
+
+    const f32x4_t *src = reinterpret_cast<const f32x4_t *>(phi + (int64_t)j * K + k0);
+    const f32x4_t p0 = src[0], p1 = src[1];
+    float b[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+    if (gamma != nullptr) {
+        const f32x4_t *gs = reinterpret_cast<const f32x4_t *>(gamma + k0);
+        const f32x4_t g0 = gs[0], g1 = gs[1];
+        const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            b[e] = b[e] * g[e];
+        }
+    }
+    float out[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float hi = bf16_bits_to_f32(f32_to_bf16_bits(b[e]));
+        out[e] = isLo ? (b[e] - hi) : hi;
+    }
+    bsplit[idx] = pack8_bf16(out);
+}
+
+// ---------------------------------------------------------------------------
+// gemm_partial: one workgroup = 4 waves = one 16-row tile x one K-slice.
+// Waves interleave the slice's 32-wide k-steps; the workgroup reduces its
+// waves through LDS in wave order and writes
+//   partial[slice][row][j]  j < M : sum over the slice of xg . B (hi + lo)
+//   partial[slice][row][M]        : sum over the slice of x^2
+// A fragment (lane l): x[row0 + l%16][32ks + 8(l/16) .. +8], one 16-byte load.
+// C fragment (lane l, reg i): C[4(l/16) + i][l%16].
+// ---------------------------------------------------------------------------
+template <int N, bool kBf16>
+__global__ __launch_bounds__(256) void gemm_partial_kernel(const uint16_t *__restrict__ x,
+                                                           const u32x4_t *__restrict__ bsplit,
+                                                           float *__restrict__ partial, int64_t T,
+                                                           int64_t K, int ksPerSlice)
+{
+    using S = Shape<N>;
+    constexpr int M = S::M;
+    constexpr int NT = S::NT;
+    constexpr int LDW = 2 * M + 1;  // LDS row stride (floats): [hi | lo] columns + sumsq
+    __shared__ float red[4][16][LDW];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (lane & 15);
+    const bool rowOk = row < T;
+    const int slice = blockIdx.y;
+    const int64_t ksTotal = K / 32;
+    const int64_t ksBegin = (int64_t)slice * ksPerSlice;
+    const int64_t ksEnd = ksBegin + ksPerSlice < ksTotal ? ksBegin + ksPerSlice : ksTotal;
+
+    f32x4_t acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    float ss = 0.f;
+    const uint16_t *xrow = x + (rowOk ? row : 0) * K + 8 * g;
+
+    for (int64_t ks = ksBegin + wave; ks < ksEnd; ks += 4) {
+        u32x4_t xa = u32x4_t{0u, 0u, 0u, 0u};
+        if (rowOk) {
+            xa = *reinterpret_cast<const u32x4_t *>(xrow + ks * 32);
+        }
+        u32x4_t bfrag[NT];
+        const u32x4_t *bsrc = bsplit + (ks * NT) * kWave + lane;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            bfrag[t] = bsrc[t * kWave];
+        }
+        float f[8];
+        unpack8<kBf16>(xa, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float sq = f[e] * f[e];
+            ss = ss + sq;
+        }
+        if constexpr (kBf16) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                acc[t] = mfma16(xa, bfrag[t], acc[t]);
+            }
+        } else {
+            u32x4_t ahi, alo;
+            split_f16_to_bf16(f, ahi, alo);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                acc[t] = mfma16(ahi, bfrag[t], acc[t]);
+            }
+#pragma unroll
+            for (int t = 0; t < S::NTHI; ++t) {
+                acc[t] = mfma16(alo, bfrag[t], acc[t]);
+            }
+        }
+    }
+
+    // Row sum of squares: the 4 lane groups of a row, fixed pairing order.
+    ss = ss + __shfl_xor(ss, 16);
+    ss = ss + __shfl_xor(ss, 32);
+
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            red[wave][4 * g + i][16 * t + (lane & 15)] = acc[t][i];
+        }
+    }
+    if (g == 0) {
+        red[wave][lane & 15][2 * M] = ss;
+    }
+    __syncthreads();
+
+    const int64_t rowBase = (int64_t)blockIdx.x * 16;
+    float *dst = partial + ((int64_t)slice * T) * (M + 1);
+    for (int idx = threadIdx.x; idx < 16 * (M + 1); idx += blockDim.x) {
+        const int r = idx / (M + 1);
+        const int j = idx % (M + 1);
+        if (rowBase + r >= T) {
+            continue;
+        }
+        float v;
+        if (j < M) {
+            v = (red[0][r][j] + red[0][r][M + j]);
+            v = v + (red[1][r][j] + red[1][r][M + j]);
+            v = v + (red[2][r][j] + red[2][r][M + j]);
+            v = v + (red[3][r][j] + red[3][r][M + j]);
+        } else {
+            v = ((red[0][r][2 * M] + red[1][r][2 * M]) + red[2][r][2 * M]) + red[3][r][2 * M];
+        }
+        dst[(rowBase + r) * (M + 1) + j] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// epilogue_hin: one workgroup per row.  Reduces the split-K partials in slice
+// order, then the epilogue (code/op_kernel/mhc_pre.cpp:735-758) and the
+// weighted stream reduction with RNE stores (code/op_kernel/mhc_pre.cpp:761-826).
+// ---------------------------------------------------------------------------
+template <int N, bool kBf16>
+__global__ __launch_bounds__(256) void epilogue_hin_kernel(
+    const uint16_t *__restrict__ x, const float *__restrict__ partial, int S, int64_t T,
+    int64_t D, const float *__restrict__ alpha, const float *__restrict__ bias, float normEps,
+    float hcEps, float invFlatDim, uint16_t *__restrict__ hIn, float *__restrict__ hPost,
+    float *__restrict__ hRes, float *__restrict__ hPre)
+{
+    constexpr int M = Shape<N>::M;
+    __shared__ float smix[M + 1];
+    __shared__ float spre[N];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+
+    if (tid <= M) {
+        float a = 0.f;
+        for (int s = 0; s < S; ++s) {
+            a = a + partial[((int64_t)s * T + row) * (M + 1) + tid];
+        }
+        smix[tid] = a;
+    }
+    __syncthreads();
+
+    if (tid < M) {
+        const float invRms = ref_inv_rms(smix[M], invFlatDim, normEps);
+        const float mix = smix[tid];
+        if (tid < N) {
+            const float sP = invRms * alpha[0];
+            const float v = ref_sigmoid(mix * sP, bias[tid], hcEps);
+            spre[tid] = v;
+            if (hPre != nullptr) {
+                hPre[row * N + tid] = v;
+            }
+        } else if (tid < 2 * N) {
+            const float sQ = invRms * alpha[1];
+            const float v = ref_sigmoid(mix * sQ, bias[tid], 0.0f);
+            hPost[row * N + (tid - N)] = v * 2.0f;
+        } else {
+            const float sR = invRms * alpha[2];
+            const float v = mix * sR;
+            hRes[row * (N * N) + (tid - 2 * N)] = v + bias[tid];
+        }
+    }
+    __syncthreads();
+
+    float pre[N];
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+        pre[s] = spre[s];
+    }
+    const uint16_t *xr = x + row * (N * D);
+    uint16_t *out = hIn + row * D;
+    for (int64_t d8 = tid; d8 < D / 8; d8 += blockDim.x) {
+        float acc[8];
+        {
+            float f[8];
+            unpack8<kBf16>(*reinterpret_cast<const u32x4_t *>(xr + d8 * 8), f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                acc[e] = pre[0] * f[e];
+            }
+        }
+#pragma unroll
+        for (int s = 1; s < N; ++s) {
+            float f[8];
+            unpack8<kBf16>(*reinterpret_cast<const u32x4_t *>(xr + s * D + d8 * 8), f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float p = pre[s] * f[e];
+                acc[e] = acc[e] + p;
+            }
+        }
+        u32x4_t o;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            o[w] = f32_to_x<kBf16>(acc[2 * w]) | (f32_to_x<kBf16>(acc[2 * w + 1]) << 16);
+        }
+        *reinterpret_cast<u32x4_t *>(out + d8 * 8) = o;
+    }
+}
+
+template <int N, bool kBf16>
+hipError_t launch_split_t(const Plan &p, void *workspace, hipStream_t stream)
+{
+    char *ws = static_cast<char *>(workspace);
+    uint32_t *status = reinterpret_cast<uint32_t *>(ws);
+    u32x4_t *bsplit = reinterpret_cast<u32x4_t *>(ws + p.wsBsplit);
+    float *partial = reinterpret_cast<float *>(ws + p.wsPartial);
+
+    const int64_t prepThreads = (p.K / 32) * p.NT * kWave;
+    hipLaunchKernelGGL(prep_b_kernel, dim3((unsigned)((prepThreads + 255) / 256)), dim3(256), 0,
+                       stream, p.phi, p.hasGamma ? p.gamma : nullptr, bsplit, p.K, p.M, p.NT,
+                       status);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    const unsigned rowTiles = (unsigned)((p.T + 15) / 16);
+    hipLaunchKernelGGL((gemm_partial_kernel<N, kBf16>), dim3(rowTiles, (unsigned)p.splitS),
+                       dim3(256), 0, stream, static_cast<const uint16_t *>(p.x), bsplit, partial,
+                       p.T, p.K, p.ksPerSlice);
+    err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+    hipLaunchKernelGGL((epilogue_hin_kernel<N, kBf16>), dim3((unsigned)p.T), dim3(256), 0, stream,
+                       static_cast<const uint16_t *>(p.x), partial, p.splitS, p.T, p.D, p.alpha,
+                       p.bias, p.normEps, p.hcEps, p.invFlatDim,
+                       static_cast<uint16_t *>(p.hIn), p.hPost, p.hRes,
+                       p.hasHPre ? p.hPre : nullptr);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_split(const Plan &p, void *workspace, hipStream_t stream)
+{
+    switch (p.n) {
+    case 4:
+        return p.isBf16 ? launch_split_t<4, true>(p, workspace, stream)
+                        : launch_split_t<4, false>(p, workspace, stream);
+    case 6:
+        return p.isBf16 ? launch_split_t<6, true>(p, workspace, stream)
+                        : launch_split_t<6, false>(p, workspace, stream);
+    case 8:
+        return p.isBf16 ? launch_split_t<8, true>(p, workspace, stream)
+                        : launch_split_t<8, false>(p, workspace, stream);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_fused(const Plan &, void *, hipStream_t) { return hipErrorNotSupported; }
+
+int fused_max_coresident(const Plan &, int) { return -1; }
+
+}  // namespace mhc

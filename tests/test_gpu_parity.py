@@ -1,0 +1,213 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Tolerances (tests/helpers.py): hPre/hPost/hRes rtol 1e-4, atol 1e-5; hIn
+within 1 ulp of the output dtype.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import assert_close_f32, assert_hin_close, ulp_distance
+from inputs import (CONFIGS, E3_ALPHA, E3_CASES, audit_formula_case, audit_formula_cases,
+                    make_case, to_bits)
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def to_device(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, lead=None):
+    import torch
+
+    dt = torch.bfloat16 if is_bf16 else torch.float16
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    if lead is not None:
+        x_bits = x_bits.reshape(tuple(lead) + x_bits.shape[-2:])
+    xt = torch.from_numpy(x_bits.view(np.int16)).to(device).view(dt)
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
+    return xt, f(phi), f(alpha), f(bias), (f(gamma) if gamma is not None else None)
+
+
+def run_gpu(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, norm_eps=1e-6, hc_eps=1e-6,
+            lead=None, h_pre=True):
+    import torch
+
+    xt, pt, at, bt, gt = to_device(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, lead)
+    op = pkg.MhcPreOp(xt, pt, at, bt, gt, norm_eps, hc_eps, h_pre=True if h_pre else None)
+    op.launch()
+    torch.cuda.synchronize()
+    assert op.device_status() == 0
+    out = fetch(op)
+    out["path"] = op.path
+    op.close()
+    return out
+
+
+def fetch(op):
+    import torch
+
+    T = op.h_in.shape[:-1].numel()
+    n = op.h_post.shape[-1]
+    out = {
+        "h_in": op.h_in.view(torch.int16).cpu().numpy().view(np.uint16).reshape(T, -1),
+        "h_post": op.h_post.cpu().numpy().reshape(T, n),
+        "h_res": op.h_res.cpu().numpy().reshape(T, n, n),
+    }
+    if op.h_pre is not None:
+        out["h_pre"] = op.h_pre.cpu().numpy().reshape(T, n)
+    return out
+
+
+def check(out, ref, rows=None):
+    sel = (lambda a: a) if rows is None else (lambda a: a[rows])
+    assert_close_f32("hPost", sel(out["h_post"]), ref["h_post"])
+    assert_close_f32("hRes", sel(out["h_res"]), ref["h_res"])
+    if "h_pre" in out:
+        assert_close_f32("hPre", sel(out["h_pre"]), ref["h_pre"])
+    assert_hin_close(sel(out["h_in"]), ref["h_in"])
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 4])
+def test_config_full_parity(pkg, orc, device, cfg):
+    case = CONFIGS[cfg]
+    _say(f"[parity] config {cfg}: {case}")
+    x, phi, alpha, bias, gamma = make_case(case)
+    out = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma)
+    ref = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
+    check(out, ref)
+
+
+@pytest.mark.parametrize("B,S,n,D,has_gamma,is_bf16", E3_CASES)
+def test_reference_e3_matrix(pkg, orc, device, B, S, n, D, has_gamma, is_bf16):
+    """The reference harness's shape matrix and inputs (cloud_runner/runner.cpp:320-382)."""
+    _say(f"[e3] B={B} S={S} n={n} D={D} gamma={has_gamma} bf16={is_bf16}")
+    T = B * S
+    xf, phi, bias, gamma = orc.reference_harness_inputs(42, T, n, D)
+    x = orc.f32_to_bits(xf, is_bf16)
+    alpha = np.asarray(E3_ALPHA, dtype=np.float32)
+    g = gamma if has_gamma else None
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, g, lead=(B, S))
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, g)
+    check(out, ref)
+    # The harness's own acceptance rule (cloud_runner/runner.cpp:279-301):
+    # |a-b| / max(1,|a|,|b|) <= 5e-2 for all but 0.1 % of elements.
+    got = orc.bits_to_f32(out["h_in"], is_bf16)
+    want = orc.bits_to_f32(ref["h_in"], is_bf16)
+    rel = np.abs(got - want) / np.maximum(1.0, np.maximum(np.abs(got), np.abs(want)))
+    assert np.count_nonzero(rel > 5e-2) <= got.size // 1000
+
+
+def test_probe_e1_e2_relaunch(pkg, orc, device):
+    """E1: first launch completes and matches; E2: a second launch of the same
+    executor matches again, bit for bit (cloud_runner/probe_e1e2.cpp:223-326)."""
+    import torch
+
+    B, S, n, D = 1, 64, 4, 256
+    xf, phi, bias, gamma = orc.reference_harness_inputs(7, B * S, n, D)
+    x = orc.f32_to_f16_bits(xf)
+    alpha = np.asarray((0.5, 0.3, 0.2), dtype=np.float32)
+    xt, pt, at, bt, gt = to_device(pkg, device, x, False, phi, alpha, bias, gamma, lead=(B, S))
+    op = pkg.MhcPreOp(xt, pt, at, bt, gt)
+    ref = orc.mhc_pre(x, False, phi, alpha, bias, gamma)
+    op.launch()
+    torch.cuda.synchronize()
+    first = fetch(op)
+    check(first, ref)
+    for t in (op.h_in, op.h_post, op.h_res):
+        t.zero_()
+    op.launch()
+    torch.cuda.synchronize()
+    second = fetch(op)
+    check(second, ref)
+    for k in first:
+        assert np.array_equal(first[k], second[k]), k
+    op.close()
+
+
+@pytest.mark.parametrize("case", audit_formula_cases())
+def test_audit_formula_cases(pkg, orc, device, case):
+    """The offline audit's 13 formula cases (audit_group_vec.py:259-344) on the GPU."""
+    n, d, has_gamma, is_bf16, rows, seed = case
+    x, phi, alpha, bias, gamma = audit_formula_case(n, d, has_gamma, is_bf16, rows, seed)
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
+    check(out, ref)
+    # The audit's own range checks (audit_group_vec.py:326-333).
+    hin = orc.bits_to_f32(out["h_in"], is_bf16)
+    assert (np.abs(hin) < 5.0).all()
+    assert ((out["h_pre"] > 0.0) & (out["h_pre"] < 1.1)).all()
+    assert (out["h_post"] > 0.0).all()
+
+
+@pytest.mark.parametrize("T,n,D,is_bf16,has_gamma", [
+    (1, 4, 16, True, True),
+    (17, 6, 48, False, True),
+    (33, 8, 64, True, False),
+    (100, 6, 1024, True, True),
+    (257, 4, 512, False, True),
+])
+def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_gamma):
+    rng = np.random.default_rng(T * 131 + n * 7 + D)
+    K, M = n * D, n * n + 2 * n
+    x = to_bits(rng.standard_normal((T, n, D)).astype(np.float32), is_bf16)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.asarray([0.3, -0.2, 0.05], dtype=np.float32)
+    bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
+    check(out, ref)
+
+
+def test_attributes_and_hpre_off(pkg, orc, device):
+    """Non-default normEps/hcEps (hcEps = 0 skips the add, mhc_pre.cpp:552) and the
+    3-output entry point (no hPre)."""
+    case = CONFIGS[1]
+    x, phi, alpha, bias, _ = make_case(case)
+    for norm_eps, hc_eps in ((1e-3, 0.0), (0.5, 0.25)):
+        out = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, None, norm_eps, hc_eps,
+                      h_pre=False)
+        ref = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, None, norm_eps, hc_eps)
+        check(out, ref)
+
+
+def test_zero_and_constant_rows(pkg, orc, device):
+    """x = 0 rows: invRms = 1/sqrt(eps), mix = 0, hIn = 0; constant rows."""
+    T, n, D = 32, 4, 256
+    K, M = n * D, n * n + 2 * n
+    rng = np.random.default_rng(5)
+    xf = np.zeros((T, n, D), dtype=np.float32)
+    xf[16:] = 0.75
+    x = to_bits(xf, True)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.full(3, 0.01, dtype=np.float32)
+    bias = rng.uniform(-0.1, 0.1, M).astype(np.float32)
+    out = run_gpu(pkg, device, x, True, phi, alpha, bias, None)
+    ref = orc.mhc_pre(x, True, phi, alpha, bias, None)
+    check(out, ref)
+    assert (ulp_distance(out["h_in"][:16], np.zeros_like(out["h_in"][:16])) == 0).all()
+
+
+def test_determinism(pkg, device):
+    """Two launches give bitwise-identical outputs (fixed-order reductions, no atomics)."""
+    import torch
+
+    case = CONFIGS[2]
+    x, phi, alpha, bias, gamma = make_case(case)
+    xt, pt, at, bt, gt = to_device(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma)
+    op = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True)
+    op.launch()
+    torch.cuda.synchronize()
+    a = fetch(op)
+    op.launch()
+    torch.cuda.synchronize()
+    b = fetch(op)
+    for k in a:
+        assert np.array_equal(a[k], b[k]), k
+    op.close()

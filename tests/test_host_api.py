@@ -1,0 +1,191 @@
+"""Host-side C ABI behaviour without a GPU: exports, validation, workspace sizing.
+
+Validation mirrors the reference TilingFunc (code/op_host/mhc_pre.cpp:57-79,
+126-130) and InferShape (:217-249); phase 1 never touches device memory, so
+fake (aligned) device addresses are enough here.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import pytest
+
+FAKE = 0x100000  # aligned placeholder device address; never dereferenced on the host
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg.load_library()
+
+
+def _descs(pkg, B=1, S=4, n=4, D=64, xdt=None, gamma=True, **over):
+    f32, xdt = pkg.MHC_DTYPE_FLOAT, (pkg.MHC_DTYPE_BF16 if xdt is None else xdt)
+    K, M = n * D, n * n + 2 * n
+    d = {
+        "x": (FAKE, xdt, [B, S, n, D]),
+        "phi": (FAKE, f32, [K, M]),
+        "alpha": (FAKE, f32, [3]),
+        "bias": (FAKE, f32, [M]),
+        "gamma": (FAKE, f32, [n, D]) if gamma else None,
+        "hIn": (FAKE, xdt, [B, S, D]),
+        "hPost": (FAKE, f32, [B, S, n]),
+        "hRes": (FAKE, f32, [B, S, n, n]),
+    }
+    d.update(over)
+    return d
+
+
+def _call(pkg, lib, d, norm_eps=1e-6, hc_eps=1e-6, h_pre=None):
+    mk = lambda v: None if v is None else ctypes.byref(pkg.make_tensor(*v))
+    ws = ctypes.c_uint64(0)
+    exe = ctypes.c_void_p(None)
+    args = [mk(d["x"]), mk(d["phi"]), mk(d["alpha"]), mk(d["bias"]), mk(d["gamma"]),
+            ctypes.c_float(norm_eps), ctypes.c_float(hc_eps), mk(d["hIn"]), mk(d["hPost"]),
+            mk(d["hRes"])]
+    if h_pre is not None:
+        st = lib.mhcPreGetWorkspaceSizeWithHPre(*args, mk(h_pre), ctypes.byref(ws),
+                                                ctypes.byref(exe))
+    else:
+        st = lib.mhcPreGetWorkspaceSize(*args, ctypes.byref(ws), ctypes.byref(exe))
+    if exe.value:
+        lib.mhcPreExecutorDestroy(exe)
+    return st, int(ws.value)
+
+
+def code(pkg, name):
+    return pkg.binding.STATUS_CODE[name]
+
+
+def test_library_exports_every_declared_symbol(pkg, lib):
+    names = pkg.exported_symbols()
+    assert set(names) >= {"mhcPreGetWorkspaceSize", "mhcPre", "mhcPreExecutorDestroy"}
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_valid_call_sizes_workspace(pkg, lib):
+    st, ws = _call(pkg, lib, _descs(pkg))
+    assert st == 0 and ws > 0
+    # 3-D x [T, n, D] extension with matching 2-D/3-D outputs.
+    n, D, T = 4, 64, 4
+    d = _descs(pkg, x=(FAKE, pkg.MHC_DTYPE_BF16, [T, n, D]),
+               hIn=(FAKE, pkg.MHC_DTYPE_BF16, [T, D]),
+               hPost=(FAKE, pkg.MHC_DTYPE_FLOAT, [T, n]),
+               hRes=(FAKE, pkg.MHC_DTYPE_FLOAT, [T, n, n]))
+    assert _call(pkg, lib, d) == (st, ws)
+
+
+def test_workspace_is_device_independent_and_grows_with_shape(pkg, lib):
+    _, small = _call(pkg, lib, _descs(pkg, S=16))
+    _, big = _call(pkg, lib, _descs(pkg, S=4096))
+    assert big > small > 0
+
+
+@pytest.mark.parametrize("over,want", [
+    ({"x": (FAKE, 27, [4, 4, 64])}, "MHC_STATUS_SUCCESS"),  # 3-D is accepted
+    ({"x": (FAKE, 27, [1, 1, 4, 4, 64])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"x": (FAKE, 27, [4, 64])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"x": (FAKE, 27, [0, 4, 4, 64])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"x": (FAKE, 27, [1, 4, 4, 0])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"x": (FAKE, 27, [1, 4, 5, 64])}, "MHC_STATUS_UNSUPPORTED_SHAPE"),
+    ({"x": (FAKE, 27, [1, 4, 2, 64])}, "MHC_STATUS_UNSUPPORTED_SHAPE"),
+    ({"x": (FAKE, 27, [1, 4, 4, 24])}, "MHC_STATUS_UNSUPPORTED_SHAPE"),
+    ({"x": (FAKE, 0, [1, 4, 4, 64])}, "MHC_STATUS_INVALID_DTYPE"),
+    ({"hIn": (FAKE, 1, [1, 4, 64])}, "MHC_STATUS_INVALID_DTYPE"),
+    ({"phi": (FAKE, 27, [256, 24])}, "MHC_STATUS_INVALID_DTYPE"),
+    ({"phi": (FAKE, 0, [256, 23])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"phi": (FAKE, 0, [24, 256])}, "MHC_STATUS_SUCCESS"),  # only the element count matters
+    ({"alpha": (FAKE, 0, [2])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"bias": (FAKE, 0, [25])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"gamma": (FAKE, 0, [4, 63])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"gamma": (0, 0, [0])}, "MHC_STATUS_SUCCESS"),  # size 0 => gamma off (mhc_pre.cpp:90)
+    ({"gamma": None}, "MHC_STATUS_SUCCESS"),
+    ({"hIn": (FAKE, 27, [1, 4, 65])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"hPost": (FAKE, 0, [1, 4, 5])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"hRes": (FAKE, 0, [1, 4, 16])}, "MHC_STATUS_INVALID_SHAPE"),
+    ({"hRes": (FAKE, 0, [1, 4, 4, 4])}, "MHC_STATUS_SUCCESS"),
+    ({"x": (0, 27, [1, 4, 4, 64])}, "MHC_STATUS_NULL_ARGUMENT"),
+    ({"hPost": (0, 0, [1, 4, 4])}, "MHC_STATUS_NULL_ARGUMENT"),
+    ({"x": (FAKE + 2, 27, [1, 4, 4, 64])}, "MHC_STATUS_MISALIGNED"),
+    ({"phi": (FAKE + 4, 0, [256, 24])}, "MHC_STATUS_MISALIGNED"),
+    ({"bias": (FAKE + 2, 0, [24])}, "MHC_STATUS_MISALIGNED"),
+])
+def test_validation_status_codes(pkg, lib, over, want):
+    d = _descs(pkg)
+    d.update(over)
+    st, _ = _call(pkg, lib, d)
+    assert st == code(pkg, want), (over, st)
+
+
+def test_null_descriptors_and_outputs(pkg, lib):
+    mk = lambda v: ctypes.byref(pkg.make_tensor(*v))
+    d = _descs(pkg)
+    ws = ctypes.c_uint64(0)
+    exe = ctypes.c_void_p(None)
+    st = lib.mhcPreGetWorkspaceSize(None, mk(d["phi"]), mk(d["alpha"]), mk(d["bias"]), None,
+                                    ctypes.c_float(1e-6), ctypes.c_float(1e-6), mk(d["hIn"]),
+                                    mk(d["hPost"]), mk(d["hRes"]), ctypes.byref(ws),
+                                    ctypes.byref(exe))
+    assert st == 1
+    st = lib.mhcPreGetWorkspaceSize(mk(d["x"]), mk(d["phi"]), mk(d["alpha"]), mk(d["bias"]),
+                                    None, ctypes.c_float(1e-6), ctypes.c_float(1e-6),
+                                    mk(d["hIn"]), mk(d["hPost"]), mk(d["hRes"]), None,
+                                    ctypes.byref(exe))
+    assert st == 1
+
+
+def test_hpre_extension_validation(pkg, lib):
+    d = _descs(pkg)
+    assert _call(pkg, lib, d, h_pre=(FAKE, 0, [1, 4, 4]))[0] == 0
+    assert _call(pkg, lib, d, h_pre=(FAKE, 0, [1, 4, 5]))[0] == 2
+    assert _call(pkg, lib, d, h_pre=(FAKE, 27, [1, 4, 4]))[0] == 4
+
+
+def test_launch_rejects_bad_workspace_before_any_device_work(pkg, lib):
+    mk = lambda v: ctypes.byref(pkg.make_tensor(*v))
+    d = _descs(pkg)
+    ws = ctypes.c_uint64(0)
+    exe = ctypes.c_void_p(None)
+    st = lib.mhcPreGetWorkspaceSize(mk(d["x"]), mk(d["phi"]), mk(d["alpha"]), mk(d["bias"]),
+                                    mk(d["gamma"]), ctypes.c_float(1e-6), ctypes.c_float(1e-6),
+                                    mk(d["hIn"]), mk(d["hPost"]), mk(d["hRes"]),
+                                    ctypes.byref(ws), ctypes.byref(exe))
+    assert st == 0
+    assert lib.mhcPre(None, ws, exe, None) == 5
+    assert lib.mhcPre(ctypes.c_void_p(FAKE), ctypes.c_uint64(ws.value - 1), exe, None) == 5
+    assert lib.mhcPre(ctypes.c_void_p(FAKE + 16), ws, exe, None) == 5  # not 256-aligned
+    assert lib.mhcPre(ctypes.c_void_p(FAKE), ws, None, None) == 1
+    name = ctypes.c_char_p()
+    assert lib.mhcPreExecutorPath(exe, ctypes.byref(name)) == 0
+    assert name.value in (b"split", b"fused")
+    assert lib.mhcPreExecutorDestroy(exe) == 0
+    assert lib.mhcPreExecutorDestroy(None) == 1
+
+
+def test_status_strings(lib):
+    assert lib.mhcPreStatusString(0) == b"success"
+    assert lib.mhcPreStatusString(5) == b"workspace too small"
+    assert lib.mhcPreStatusString(12345) == b"unknown status"
+
+
+def test_phase1_is_thread_safe(pkg, lib):
+    """Concurrent phase-1 calls with different shapes each get their own answer
+    (the reference's tiling cache is an unlocked global, mhc_pre.cpp:51)."""
+    shapes = [(1, S, n, D) for S in (3, 17, 64) for n in (4, 6, 8) for D in (16, 64, 256)]
+    expected = {s: _call(pkg, lib, _descs(pkg, *s)) for s in shapes}
+    errors = []
+
+    def worker(seed):
+        for i in range(40):
+            s = shapes[(seed * 7 + i) % len(shapes)]
+            got = _call(pkg, lib, _descs(pkg, *s))
+            if got != expected[s]:
+                errors.append((s, got, expected[s]))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors
