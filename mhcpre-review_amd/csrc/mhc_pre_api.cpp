@@ -16,7 +16,9 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 struct mhcPreExecutor {
@@ -51,6 +53,28 @@ bool dims_positive(const mhcTensor &t)
 bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Compute-unit count of the current device, cached per device.
+int device_cu_count(int &device)
+{
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static int cache[kMaxDevices] = {};
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+        return -1;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (cache[device] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
+                hipSuccess ||
+            cus <= 0) {
+            return -1;
+        }
+        cache[device] = cus;
+    }
+    return cache[device];
+}
 
 // Trailing dims of `t` must be `tail` and its element count `count`.
 bool shape_matches(const mhcTensor &t, int64_t count, const int64_t *tail, int ntail)
@@ -173,8 +197,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     p.hPre = hPre != nullptr ? static_cast<float *>(hPre->data) : nullptr;
 
     // Split path plan: enough (row tile, K-slice) workgroups to fill the chip,
-    // at least 16 k-steps (4 per wave) per slice.  Shape-only, so the
-    // workspace size does not depend on the device.
+    // at least 16 k-steps (4 per wave) per slice.
     const int64_t rowTiles = (T + 15) / 16;
     const int64_t ksTotal = K / 32;
     const int64_t maxSlices = std::max<int64_t>(1, ksTotal / 16);
@@ -183,15 +206,47 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     S = (ksTotal + ksPer - 1) / ksPer;
     p.splitS = static_cast<int>(S);
     p.ksPerSlice = static_cast<int>(ksPer);
-    p.path = mhc::Path::kSplit;
 
-    size_t off = mhc::kWsHeaderBytes;
-    p.wsBsplit = off;
-    off = align_up(off + static_cast<size_t>(K) * static_cast<size_t>(2 * M) * 2, 256);
-    p.wsPartial = off;
-    off = align_up(off + static_cast<size_t>(S) * static_cast<size_t>(T) * (M + 1) * 4, 256);
-    p.wsCounters = off;
-    p.wsTotal = off;
+    // Fused path (n = 4): slices of 32*KS columns, KS preferring 7 (D = 7168
+    // gives 32 slices: 8 XCD-local teams on 256 CUs), then 8, 4, 2, 1.
+    p.fusedTiles = rowTiles;
+    if (n == 4 && (D % 32) == 0) {
+        for (int ks : {7, 8, 4, 2, 1}) {
+            if (D % (32 * ks) == 0) {
+                p.fusedDw = 32 * ks;
+                p.fusedP = static_cast<int>(D / (32 * ks));
+                break;
+            }
+        }
+    }
+    p.path = p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit;
+    if (const char *force = std::getenv("MHCPRE_FORCE_PATH")) {
+        if (std::strcmp(force, "split") == 0) {
+            p.path = mhc::Path::kSplit;
+        }
+    }
+
+    // Workspace: header, then the split regions and the fused regions, which
+    // overlap (one launch at a time per workspace).  Sizes depend on the
+    // shape only, never on the device.
+    const size_t splitBsplit = mhc::kWsHeaderBytes;
+    const size_t splitPartial =
+        align_up(splitBsplit + static_cast<size_t>(K) * static_cast<size_t>(2 * M) * 2, 256);
+    const size_t splitEnd =
+        align_up(splitPartial + static_cast<size_t>(S) * static_cast<size_t>(T) * (M + 1) * 4, 256);
+    p.wsBsplit = splitBsplit;
+    p.wsPartial = splitPartial;
+    size_t fusedEnd = 0;
+    if (p.fusedP > 0) {
+        const size_t rs = static_cast<size_t>(mhc::fused_partial_row_floats(n));
+        p.wsFinal = mhc::kWsHeaderBytes;
+        p.wsFusedPartial =
+            align_up(p.wsFinal + static_cast<size_t>(rowTiles) * 16 * n * 4, 256);
+        p.wsCounters = align_up(p.wsFusedPartial + static_cast<size_t>(rowTiles) * p.fusedP * 16 *
+                                                        rs * 4, 256);
+        fusedEnd = align_up(p.wsCounters + static_cast<size_t>(rowTiles) * 2 * 4, 256);
+    }
+    p.wsTotal = std::max(splitEnd, fusedEnd);
     return MHC_STATUS_SUCCESS;
 }
 
@@ -263,15 +318,27 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
     if (!aligned(workspace, 256)) {
         return MHC_STATUS_WORKSPACE_TOO_SMALL;
     }
-    hipError_t err;
-    switch (p.path) {
-    case mhc::Path::kFused:
-        err = mhc::launch_fused(p, workspace, stream);
-        break;
-    case mhc::Path::kSplit:
-    default:
+    hipError_t err = hipSuccess;
+    bool done = false;
+    if (p.path == mhc::Path::kFused) {
+        // Teams of fusedP workgroups must be co-resident (cooperative launch);
+        // a device too small for one team runs the split path instead.
+        int device = -1;
+        const int cus = device_cu_count(device);
+        if (cus < 0) {
+            return MHC_STATUS_HIP_ERROR;
+        }
+        const int coresident = mhc::fused_max_coresident(p, cus);
+        if (coresident >= p.fusedP) {
+            mhc::Plan lp = p;
+            lp.fusedTeams = coresident / p.fusedP;
+            lp.fusedGrid = lp.fusedTeams * p.fusedP;
+            err = mhc::launch_fused(lp, workspace, stream);
+            done = true;
+        }
+    }
+    if (!done) {
         err = mhc::launch_split(p, workspace, stream);
-        break;
     }
     return err == hipSuccess ? MHC_STATUS_SUCCESS : MHC_STATUS_HIP_ERROR;
 }

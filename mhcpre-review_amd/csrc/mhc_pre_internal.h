@@ -42,18 +42,21 @@ struct Plan {
     int splitS = 1;
     int ksPerSlice = 0;
 
-    // Fused path parameters.
-    int fusedDw = 0;          // d-columns per wave slice
-    int fusedP = 0;           // waves (slices) per 16-row tile team
-    int fusedWaves = 0;       // waves per workgroup
-    int fusedGrid = 0;        // workgroups (cooperative grid)
-    int fusedTeams = 0;       // teams of fusedP slices
+    // Fused path parameters (fusedGrid / fusedTeams are filled per launch
+    // from the device's co-residency limit).
+    int fusedDw = 0;          // x columns per slice (32 * k-steps)
+    int fusedP = 0;           // slices per row tile = D / fusedDw
+    int fusedGrid = 0;        // workgroups in the cooperative grid
+    int fusedTeams = 0;       // teams of fusedP workgroups
     int64_t fusedTiles = 0;   // 16-row tiles
 
-    // Workspace layout (byte offsets).
-    size_t wsBsplit = 0;
-    size_t wsPartial = 0;
-    size_t wsCounters = 0;
+    // Workspace layout (byte offsets).  The two paths' regions overlap: a
+    // workspace holds one launch at a time.
+    size_t wsBsplit = 0;      // split: B fragments
+    size_t wsPartial = 0;     // split: [S][T][M+1] partials
+    size_t wsFinal = 0;       // fused: [RT][16][n] hPre
+    size_t wsFusedPartial = 0;// fused: [RT][P][16][RS] partials
+    size_t wsCounters = 0;    // fused: arrival + ready counters, 2 x RT
     size_t wsTotal = 0;
 
     // Bound device pointers (caller memory).
@@ -72,8 +75,15 @@ struct Plan {
 hipError_t launch_split(const Plan &plan, void *workspace, hipStream_t stream);
 hipError_t launch_fused(const Plan &plan, void *workspace, hipStream_t stream);
 
-// Largest number of fused-path workgroups that can be co-resident on the
-// current device for a plan with the given wave count, or a negative HIP error.
+// Largest number of fused-path workgroups that can be co-resident on a device
+// with numCUs compute units, or -1 if the plan has no fused kernel.
 int fused_max_coresident(const Plan &plan, int numCUs);
+
+// Floats per row of a fused-path partial record for n streams.
+inline int fused_partial_row_floats(int n)
+{
+    const int M = n * n + 2 * n;
+    return ((n + 1 + 3) / 4) * 4 + ((M - n + 3) / 4) * 4;
+}
 
 }  // namespace mhc

@@ -160,6 +160,21 @@ static float oracle_sigmoid(float scaled, float bias, float eps)
     return v;
 }
 
+/* hIn[d] = RNE(((hPre[0]*x0 + hPre[1]*x1) + ...) + hPre[n-1]*x_{n-1}) on raw x
+ * (mhc_pre.cpp:787-813: broadcast multiply, stream-ordered add, CAST_RINT). */
+static void stream_sum_row(const float *xf, int is_bf16, int n, int64_t D, const float *pre,
+                           uint16_t *h_in)
+{
+    for (int64_t d = 0; d < D; ++d) {
+        float a = pre[0] * xf[d];
+        for (int s = 1; s < n; ++s) {
+            const float p = pre[s] * xf[(int64_t)s * D + d];
+            a = a + p;
+        }
+        h_in[d] = is_bf16 ? oracle_f32_to_bf16(a) : oracle_f32_to_f16(a);
+    }
+}
+
 /* One row of the operator.  `phi_t` is phi transposed to [K][M] so the GEMM's
  * inner loop runs over the M independent accumulators; each accumulator still
  * sums its products in increasing k, one rounding per product and per add. */
@@ -231,16 +246,7 @@ static void oracle_row(const uint16_t *xrow, int is_bf16, int n, int64_t D,
         h_res[ij] = scaled + bias[2 * n + ij];
     }
 
-    /* hIn[d] = RNE(((hPre[0]*x0 + hPre[1]*x1) + ...) + hPre[n-1]*x_{n-1}) on raw x
-     * (mhc_pre.cpp:787-813: broadcast multiply, stream-ordered add, CAST_RINT). */
-    for (int64_t d = 0; d < D; ++d) {
-        float a = pre_local[0] * xf[d];
-        for (int s = 1; s < n; ++s) {
-            const float p = pre_local[s] * xf[(int64_t)s * D + d];
-            a = a + p;
-        }
-        h_in[d] = is_bf16 ? oracle_f32_to_bf16(a) : oracle_f32_to_f16(a);
-    }
+    stream_sum_row(xf, is_bf16, n, D, pre_local, h_in);
 
     if (mix_out) {
         memcpy(mix_out, acc, sizeof(float) * (size_t)M);
@@ -337,4 +343,25 @@ void oracle_reference_harness_inputs(unsigned seed, int64_t T, int n, int64_t D,
     for (int64_t i = 0; i < K; ++i) {
         gamma[i] = 1.0f + (float)(rand() % 200) / 10000.0f;
     }
+}
+
+int oracle_weighted_stream_sum(const uint16_t *x, int is_bf16, int64_t R, int n, int64_t D,
+                               const float *h_pre, uint16_t *h_in)
+{
+    if (!x || !h_pre || !h_in || n < 1 || n > 8 || D <= 0 || R < 0) {
+        return 1;
+    }
+    const int64_t K = (int64_t)n * D;
+    float *xf = (float *)malloc(sizeof(float) * (size_t)K);
+    if (!xf) {
+        return 4;
+    }
+    for (int64_t r = 0; r < R; ++r) {
+        for (int64_t k = 0; k < K; ++k) {
+            xf[k] = is_bf16 ? oracle_bf16_to_f32(x[r * K + k]) : oracle_f16_to_f32(x[r * K + k]);
+        }
+        stream_sum_row(xf, is_bf16, n, D, h_pre + r * n, h_in + r * D);
+    }
+    free(xf);
+    return 0;
 }

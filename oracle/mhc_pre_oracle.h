@@ -62,6 +62,16 @@ int oracle_mhc_pre(const uint16_t *x, int is_bf16, int64_t T, int n, int64_t D,
                    uint16_t *h_in, float *h_post, float *h_res, float *h_pre,
                    float *mix, float *inv_rms, int nthreads);
 
+/*
+ * The weighted stream reduction alone, on given hPre weights:
+ *   hIn[r][d] = RNE(sum_s fl(hPre[r][s] * x[r][s][d])), streams in order
+ * (the same code path oracle_mhc_pre uses).  x [R][n][D] 16-bit patterns,
+ * h_pre [R][n], h_in [R][D].  Lets a test check a device's hIn stage
+ * bit-exactly from the device's own hPre.
+ */
+int oracle_weighted_stream_sum(const uint16_t *x, int is_bf16, int64_t R, int n, int64_t D,
+                               const float *h_pre, uint16_t *h_in);
+
 /* Number of threads oracle_mhc_pre uses for nthreads <= 0. */
 int oracle_max_threads(void);
 

@@ -45,6 +45,9 @@ def _load() -> ctypes.CDLL:
                                    f32p, f32p, f32p, ctypes.c_int]
     lib.oracle_mhc_pre.restype = ctypes.c_int
     lib.oracle_max_threads.restype = ctypes.c_int
+    lib.oracle_weighted_stream_sum.argtypes = [u16p, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
+                                               ctypes.c_int64, f32p, u16p]
+    lib.oracle_weighted_stream_sum.restype = ctypes.c_int
     lib.oracle_reference_harness_inputs.argtypes = [ctypes.c_uint, ctypes.c_int64, ctypes.c_int,
                                                     ctypes.c_int64, f32p, f32p, f32p, f32p]
     _lib = lib
@@ -145,6 +148,21 @@ def mhc_pre(x_bits: np.ndarray, is_bf16: bool, phi: np.ndarray, alpha, bias, gam
         _ptr(out["mix"], ctypes.c_float), _ptr(out["inv_rms"], ctypes.c_float), int(nthreads))
     if st != 0:
         raise RuntimeError(f"oracle_mhc_pre failed with {st}")
+    return out
+
+
+def weighted_stream_sum(x_bits: np.ndarray, is_bf16: bool, h_pre: np.ndarray) -> np.ndarray:
+    """hIn from given hPre weights in the reference order (oracle_weighted_stream_sum)."""
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    x_bits = x_bits.reshape((-1,) + x_bits.shape[-2:])
+    R, n, D = (int(v) for v in x_bits.shape)
+    h_pre = np.ascontiguousarray(h_pre, dtype=np.float32).reshape(R, n)
+    out = np.empty((R, D), dtype=np.uint16)
+    st = _load().oracle_weighted_stream_sum(_ptr(x_bits, ctypes.c_uint16), int(bool(is_bf16)), R,
+                                            n, D, _ptr(h_pre, ctypes.c_float),
+                                            _ptr(out, ctypes.c_uint16))
+    if st != 0:
+        raise RuntimeError(f"oracle_weighted_stream_sum failed with {st}")
     return out
 
 

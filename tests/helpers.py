@@ -1,7 +1,17 @@
 """Comparison helpers: the tolerances every parity test applies.
 
 hPre / hPost / hRes (fp32): |got - want| <= 1e-5 + 1e-4 * |want|.
-hIn (fp16 / bf16):          at most 1 unit in the last place of the output dtype.
+hIn (fp16 / bf16):
+  * the device's weighted stream reduction is bit-exact: hIn equals
+    RNE(sum_s fl(hPre[s] * x[s])) evaluated by the oracle, in the reference's
+    stream order, on the device's own hPre;
+  * against the oracle's hIn, at most 1 unit in the last place of the output
+    dtype -- except where the sum cancels so far that the (tolerated) fp32
+    difference between the device's and the oracle's hPre moves it further.
+    Those elements must still lie within 1 ulp plus sum_s |dhPre[s] * x[s]|,
+    and they must be rare (at most 1 in 10^4).  The GEMM's summation order is
+    hardware-defined in the reference (CANN Cube) and cannot be matched, so
+    hPre agrees to fp32 rounding, not bit for bit.
 """
 from __future__ import annotations
 
@@ -49,3 +59,53 @@ def assert_hin_close(got_bits: np.ndarray, want_bits: np.ndarray,
         i = np.unravel_index(np.argmax(d), d.shape)
         raise AssertionError(f"hIn: {int((d > max_ulp).sum())}/{d.size} beyond {max_ulp} ulp; "
                              f"worst {int(d[i])} ulp at {i}")
+
+
+def _decode16(bits: np.ndarray, is_bf16: bool) -> np.ndarray:
+    bits = np.asarray(bits, dtype=np.uint16)
+    if is_bf16:
+        return (bits.astype(np.uint32) << np.uint32(16)).view(np.float32).astype(np.float64)
+    return bits.view(np.float16).astype(np.float64)
+
+
+def _ulp16(bits: np.ndarray, is_bf16: bool) -> np.ndarray:
+    mag = np.asarray(bits, dtype=np.uint16) & np.uint16(0x7FFF)
+    nxt = np.minimum(mag.astype(np.uint32) + 1, 0x7FFF).astype(np.uint16)
+    return np.abs(_decode16(nxt, is_bf16) - _decode16(mag, is_bf16))
+
+
+def assert_hin(got_bits, want_bits, x_bits, is_bf16: bool, got_pre, want_pre, orc,
+               max_rare_fraction: float = 1e-4) -> None:
+    """hIn check (see the module docstring).  got_pre=None when the device did
+    not return hPre: the bound then uses the hPre tolerance instead."""
+    got_bits = np.ascontiguousarray(got_bits).view(np.uint16)
+    want_bits = np.ascontiguousarray(want_bits, dtype=np.uint16)
+    R, D = want_bits.shape
+    x_bits = np.ascontiguousarray(x_bits, dtype=np.uint16).reshape(R, -1, D)
+    assert got_bits.shape == want_bits.shape, (got_bits.shape, want_bits.shape)
+    if got_pre is not None:
+        got_pre = np.asarray(got_pre, dtype=np.float32).reshape(R, -1)
+        exact = orc.weighted_stream_sum(x_bits, is_bf16, got_pre)
+        neq = got_bits != exact
+        if neq.any():
+            i = np.unravel_index(np.argmax(neq), neq.shape)
+            raise AssertionError(f"hIn stage: {int(neq.sum())}/{neq.size} differ from the "
+                                 f"reference stream sum on the device hPre; first at {i}")
+        dpre = np.abs(got_pre.astype(np.float64) - np.asarray(want_pre, np.float64).reshape(R, -1))
+    else:
+        wp = np.abs(np.asarray(want_pre, np.float64).reshape(R, -1))
+        dpre = ATOL + RTOL * wp
+    d = ulp_distance(got_bits, want_bits)
+    far = d > HIN_MAX_ULP
+    if far.any():
+        xf = np.abs(_decode16(x_bits, is_bf16))                      # [R, n, D]
+        bound = (dpre[:, :, None] * xf).sum(1) * (1 + 1e-6) + _ulp16(want_bits, is_bf16)
+        diff = np.abs(_decode16(got_bits, is_bf16) - _decode16(want_bits, is_bf16))
+        bad = far & (diff > bound)
+        if bad.any():
+            i = np.unravel_index(np.argmax(bad), bad.shape)
+            raise AssertionError(f"hIn: {int(bad.sum())} elements beyond 1 ulp + hPre "
+                                 f"propagation; first at {i}: diff {diff[i]:.3e} "
+                                 f"bound {bound[i]:.3e} ({int(d[i])} ulp)")
+        frac = far.sum() / far.size
+        assert frac <= max_rare_fraction, f"hIn: {frac:.2e} of elements beyond 1 ulp"

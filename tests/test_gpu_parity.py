@@ -10,7 +10,7 @@ import sys
 import numpy as np
 import pytest
 
-from helpers import assert_close_f32, assert_hin_close, ulp_distance
+from helpers import assert_close_f32, assert_hin, ulp_distance
 from inputs import (CONFIGS, E3_ALPHA, E3_CASES, audit_formula_case, audit_formula_cases,
                     make_case, to_bits)
 
@@ -35,11 +35,19 @@ def to_device(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, lead=None):
 
 
 def run_gpu(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, norm_eps=1e-6, hc_eps=1e-6,
-            lead=None, h_pre=True):
+            lead=None, h_pre=True, force_path=None):
+    import os
+
     import torch
 
     xt, pt, at, bt, gt = to_device(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, lead)
-    op = pkg.MhcPreOp(xt, pt, at, bt, gt, norm_eps, hc_eps, h_pre=True if h_pre else None)
+    if force_path is not None:
+        os.environ["MHCPRE_FORCE_PATH"] = force_path
+    try:
+        op = pkg.MhcPreOp(xt, pt, at, bt, gt, norm_eps, hc_eps, h_pre=True if h_pre else None)
+    finally:
+        os.environ.pop("MHCPRE_FORCE_PATH", None)
+    _say(f"  path={op.path}")
     op.launch()
     torch.cuda.synchronize()
     assert op.device_status() == 0
@@ -64,23 +72,23 @@ def fetch(op):
     return out
 
 
-def check(out, ref, rows=None):
-    sel = (lambda a: a) if rows is None else (lambda a: a[rows])
-    assert_close_f32("hPost", sel(out["h_post"]), ref["h_post"])
-    assert_close_f32("hRes", sel(out["h_res"]), ref["h_res"])
+def check(out, ref, x_bits, is_bf16, orc):
+    assert_close_f32("hPost", out["h_post"], ref["h_post"])
+    assert_close_f32("hRes", out["h_res"], ref["h_res"])
     if "h_pre" in out:
-        assert_close_f32("hPre", sel(out["h_pre"]), ref["h_pre"])
-    assert_hin_close(sel(out["h_in"]), ref["h_in"])
+        assert_close_f32("hPre", out["h_pre"], ref["h_pre"])
+    assert_hin(out["h_in"], ref["h_in"], x_bits, is_bf16, out.get("h_pre"), ref["h_pre"], orc)
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 4])
-def test_config_full_parity(pkg, orc, device, cfg):
+@pytest.mark.parametrize("cfg,force", [(1, None), (2, None), (4, None), (1, "split"),
+                                       (2, "split")])
+def test_config_full_parity(pkg, orc, device, cfg, force):
     case = CONFIGS[cfg]
-    _say(f"[parity] config {cfg}: {case}")
+    _say(f"[parity] config {cfg} force={force}: {case}")
     x, phi, alpha, bias, gamma = make_case(case)
-    out = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma)
+    out = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, force_path=force)
     ref = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
-    check(out, ref)
+    check(out, ref, x, case.is_bf16, orc)
 
 
 @pytest.mark.parametrize("B,S,n,D,has_gamma,is_bf16", E3_CASES)
@@ -94,7 +102,7 @@ def test_reference_e3_matrix(pkg, orc, device, B, S, n, D, has_gamma, is_bf16):
     g = gamma if has_gamma else None
     out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, g, lead=(B, S))
     ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, g)
-    check(out, ref)
+    check(out, ref, x, is_bf16, orc)
     # The harness's own acceptance rule (cloud_runner/runner.cpp:279-301):
     # |a-b| / max(1,|a|,|b|) <= 5e-2 for all but 0.1 % of elements.
     got = orc.bits_to_f32(out["h_in"], is_bf16)
@@ -118,13 +126,13 @@ def test_probe_e1_e2_relaunch(pkg, orc, device):
     op.launch()
     torch.cuda.synchronize()
     first = fetch(op)
-    check(first, ref)
+    check(first, ref, x, False, orc)
     for t in (op.h_in, op.h_post, op.h_res):
         t.zero_()
     op.launch()
     torch.cuda.synchronize()
     second = fetch(op)
-    check(second, ref)
+    check(second, ref, x, False, orc)
     for k in first:
         assert np.array_equal(first[k], second[k]), k
     op.close()
@@ -137,7 +145,7 @@ def test_audit_formula_cases(pkg, orc, device, case):
     x, phi, alpha, bias, gamma = audit_formula_case(n, d, has_gamma, is_bf16, rows, seed)
     out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
     ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
-    check(out, ref)
+    check(out, ref, x, is_bf16, orc)
     # The audit's own range checks (audit_group_vec.py:326-333).
     hin = orc.bits_to_f32(out["h_in"], is_bf16)
     assert (np.abs(hin) < 5.0).all()
@@ -151,6 +159,9 @@ def test_audit_formula_cases(pkg, orc, device, case):
     (33, 8, 64, True, False),
     (100, 6, 1024, True, True),
     (257, 4, 512, False, True),
+    (333, 4, 7168, True, True),
+    (49, 4, 1792, False, False),
+    (1000, 4, 64, True, True),
 ])
 def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     rng = np.random.default_rng(T * 131 + n * 7 + D)
@@ -162,7 +173,7 @@ def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_ga
     gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
     out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
     ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
-    check(out, ref)
+    check(out, ref, x, is_bf16, orc)
 
 
 def test_attributes_and_hpre_off(pkg, orc, device):
@@ -174,7 +185,7 @@ def test_attributes_and_hpre_off(pkg, orc, device):
         out = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, None, norm_eps, hc_eps,
                       h_pre=False)
         ref = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, None, norm_eps, hc_eps)
-        check(out, ref)
+        check(out, ref, x, case.is_bf16, orc)
 
 
 def test_zero_and_constant_rows(pkg, orc, device):
@@ -190,7 +201,7 @@ def test_zero_and_constant_rows(pkg, orc, device):
     bias = rng.uniform(-0.1, 0.1, M).astype(np.float32)
     out = run_gpu(pkg, device, x, True, phi, alpha, bias, None)
     ref = orc.mhc_pre(x, True, phi, alpha, bias, None)
-    check(out, ref)
+    check(out, ref, x, True, orc)
     assert (ulp_distance(out["h_in"][:16], np.zeros_like(out["h_in"][:16])) == 0).all()
 
 

@@ -302,3 +302,15 @@ def test_golden_fixture_config1(orc):
     out = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
     for k in ("h_in", "h_post", "h_res", "h_pre"):
         assert np.array_equal(out[k], data[k]), k
+
+
+def test_weighted_stream_sum_is_the_oracle_hin_stage(orc):
+    """oracle.weighted_stream_sum on the oracle's own hPre reproduces its hIn bit
+    for bit (the GPU tests use it to check the device's hIn stage exactly)."""
+    for cfg in (1, 2):
+        case = CONFIGS[cfg]
+        x, phi, alpha, bias, gamma = make_case(case)
+        x = x[:64]
+        out = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
+        again = orc.weighted_stream_sum(x, case.is_bf16, out["h_pre"])
+        assert np.array_equal(again, out["h_in"])
