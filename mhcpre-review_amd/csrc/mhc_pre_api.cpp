@@ -238,13 +238,12 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     p.wsPartial = splitPartial;
     size_t fusedEnd = 0;
     if (p.fusedP > 0) {
-        const size_t rs = static_cast<size_t>(mhc::fused_partial_row_floats(n));
         p.wsFinal = mhc::kWsHeaderBytes;
-        p.wsFusedPartial =
-            align_up(p.wsFinal + static_cast<size_t>(rowTiles) * 16 * n * 4, 256);
-        p.wsCounters = align_up(p.wsFusedPartial + static_cast<size_t>(rowTiles) * p.fusedP * 16 *
-                                                        rs * 4, 256);
-        fusedEnd = align_up(p.wsCounters + static_cast<size_t>(rowTiles) * 2 * 4, 256);
+        p.wsFusedPartial = align_up(
+            p.wsFinal + static_cast<size_t>(rowTiles) * mhc::fused_final_floats(n) * 4, 256);
+        p.wsCounters = align_up(p.wsFusedPartial + static_cast<size_t>(rowTiles) * p.fusedP *
+                                                        mhc::fused_record_floats(n) * 4, 256);
+        fusedEnd = p.wsCounters + static_cast<size_t>(rowTiles) * mhc::kFusedCounterBytes;
     }
     p.wsTotal = std::max(splitEnd, fusedEnd);
     return MHC_STATUS_SUCCESS;

@@ -10,8 +10,6 @@ namespace dev {
 typedef __bf16 bf16x8_t __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef float f32x4_t __attribute__((__vector_size__(4 * sizeof(float))));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
@@ -73,22 +71,50 @@ __device__ __forceinline__ u32x4_t pack8_bf16(const float (&f)[8])
     return r;
 }
 
-// acc + sum of the squares of 8 packed 16-bit values, two per v_dot2 (the
-// products of two 16-bit floats are exact in fp32).
+// acc + sum of the squares of 8 packed 16-bit values, one fp32 FMA per value
+// (unpacking a bf16 pair is one shift and one mask).
 template <bool kBf16>
 __device__ __forceinline__ float sumsq8(const u32x4_t &v, float acc)
 {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
+        float lo, hi;
         if constexpr (kBf16) {
-            const bf16x2_t p = __builtin_bit_cast(bf16x2_t, v[w]);
-            acc = __builtin_amdgcn_fdot2_f32_bf16(p, p, acc, false);
+            lo = __uint_as_float(v[w] << 16);
+            hi = __uint_as_float(v[w] & 0xFFFF0000u);
         } else {
-            const f16x2_t p = __builtin_bit_cast(f16x2_t, v[w]);
-            acc = __builtin_amdgcn_fdot2(p, p, acc, false);
+            lo = f16_bits_to_f32(v[w] & 0xFFFFu);
+            hi = f16_bits_to_f32(v[w] >> 16);
         }
+        acc = __builtin_fmaf(lo, lo, acc);
+        acc = __builtin_fmaf(hi, hi, acc);
     }
     return acc;
+}
+
+// Device-scope (cross-XCD coherent) accesses for data exchanged between
+// workgroups inside one launch: global_store / global_load with the sc1
+// scope bit.  They write through / read past the per-XCD L2 without the
+// whole-cache write-back and invalidate that an agent-scope fence costs.
+__device__ __forceinline__ void st_dev(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float ld_dev(const float *p)
+{
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until every memory access this wave issued has completed (stores
+// acknowledged at their scope), and keeps the compiler from moving memory
+// accesses across the wait.  Placed between the device-scope data stores and
+// the atomic that publishes them.
+__device__ __forceinline__ void wait_all_memory()
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t &v) { return __builtin_bit_cast(bf16x8_t, v); }

@@ -14,16 +14,21 @@
 //      sums x^2 from the same registers;
 //   2. publishes the slice's partial sums (M mix columns + sumsq per row) and
 //      counts itself in on the row tile's arrival counter;
-//   3. the last of the P slices to arrive reduces the hPre columns and sumsq
-//      over all slices in slice order, evaluates invRms and hPre, publishes
-//      them and raises the row tile's flag; then it reduces the remaining
-//      columns and writes hPost / hRes (and hPre when asked);
-//      every other slice waits for the flag and reads hPre;
+//   3. the last of the P slices to arrive sums the hPre columns and sumsq
+//      over all slices in a fixed order, evaluates invRms and hPre and
+//      publishes hPre; then it sums the remaining columns and writes hPost /
+//      hRes (and hPre when asked); every other slice polls the published hPre
+//      of its rows;
 //   4. computes hIn for its DW columns from the x still in its registers.
 // The last-arriver rule needs no wave to wait for one that has not arrived,
 // and the cooperative launch keeps every workgroup resident, so the waits
 // always end; each is still bounded by a spin limit that records
 // kDeviceTimeout in the status word instead of hanging.
+//
+// Exchange memory is accessed with device-scope (sc1) loads and stores, and a
+// wave waits for its stores to complete (s_waitcnt) before the atomic that
+// announces them; no agent-scope fence is used, because on a multi-L2 device
+// each one writes back or invalidates a whole L2.
 
 #include "mhc_pre_device.h"
 #include "mhc_pre_internal.h"
@@ -50,10 +55,9 @@ struct FusedArgs {
     float *hPost;
     float *hRes;
     float *hPre;
-    float *partial;      // [RT][P][16][RS]
-    float *finalPre;     // [RT][16][N]
-    uint32_t *arrive;    // [RT]
-    uint32_t *ready;     // [RT]
+    float *partial;      // [RT][P] records of Rec<N>::FLOATS
+    float *finalPre;     // [RT] blocks of Rec<N>::FIN
+    uint32_t *arrive;    // [RT] counters, kCounterStride words apart
     uint32_t *status;
     int64_t T;
     int64_t D;
@@ -94,24 +98,62 @@ struct ColLayout {
     static constexpr bool has_hi(int t) { return t < Q || t == 2 * Q; }
 };
 
-// Partial row layout (floats): [0,N) hPre columns, N sumsq, padded to PF; then
-// the other M - N columns, padded to RS.
+// Exchange record of one (row tile, slice), column-major: column c holds its
+// 16 rows contiguously (64 bytes).  Column N is the sum of squares; mix column
+// j sits at column j (j < N, the hPre columns) or j + 1.  The column count is
+// even, so a record is a whole number of 128-byte lines and no line is
+// written by two slices.  A wave reads four columns of 16 rows -- one 256-byte
+// span -- per load instruction.
 template <int N>
-struct PartLayout {
+struct Rec {
     static constexpr int M = N * N + 2 * N;
-    static constexpr int PF = ((N + 1 + 3) / 4) * 4;
-    static constexpr int RS = PF + ((M - N + 3) / 4) * 4;
-    __device__ static int off(int j) { return j < N ? j : PF + (j - N); }
+    static constexpr int RC = ((M + 1 + 1) / 2) * 2;
+    static constexpr int FLOATS = RC * 16;
+    // Per-tile broadcast block written by the last slice: hPre columns
+    // 0..N-1 and invRms at column N, 16 rows each, padded to 128-byte lines.
+    static constexpr int FIN = (((N + 1) * 16 + 31) / 32) * 32;
+    __device__ static int col(int j) { return j < N ? j : j + 1; }
 };
 
+// Arrival counters are spaced one 256-byte line apart: device-scope atomics
+// on one line serialize, and the tiles' counters are hit concurrently.
+constexpr int kCounterStride = 64;  // uint32 words
+
+// hPre slots not yet written hold this signalling-NaN pattern; arithmetic
+// only ever produces quiet NaNs, so a computed hPre can never equal it.
+constexpr uint32_t kPreSentinel = 0x7F80DEADu;
+
+// Sum over slices q = 0..P-1, in that order, of the float at src + q*step;
+// loads are issued 32 slices at a time so they are in flight together.
+__device__ __forceinline__ float sum_over_slices(const float *src, int P, int step, bool active)
+{
+    float v = 0.f;
+    for (int q0 = 0; q0 < P; q0 += 32) {
+        float t[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+            const int q = q0 + u;
+            t[u] = (active && q < P) ? ld_dev(src + (int64_t)q * step) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+            v = v + t[u];
+        }
+    }
+    return v;
+}
+
 __global__ __launch_bounds__(256) void fused_reset_kernel(uint32_t *__restrict__ arrive,
-                                                          uint32_t *__restrict__ ready, int64_t RT,
+                                                          uint32_t *__restrict__ finalPre,
+                                                          int64_t RT, int64_t finalWords,
                                                           uint32_t *__restrict__ status)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < RT) {
-        arrive[i] = 0u;
-        ready[i] = 0u;
+        arrive[i * kCounterStride] = 0u;
+    }
+    if (i < finalWords) {
+        finalPre[i] = kPreSentinel;
     }
     if (i == 0) {
         *status = kDeviceOk;
@@ -125,10 +167,9 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     constexpr int M = S::M;
     constexpr int NT = S::NT;
     using CL = ColLayout<M>;
-    using PL = PartLayout<N>;
+    using RC = Rec<N>;
     constexpr int W = kFusedWaves;
     constexpr int DW = 32 * KS;
-    constexpr int NFRAG = N * KS * NT;
     constexpr int Q = CL::Q;
     extern __shared__ u32x4_t bl[];  // [NFRAG][64] B fragments of this workgroup's slice
 
@@ -163,42 +204,74 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
             }
         }
     };
+    if ((int64_t)team * W >= a.RT) {
+        return;  // no row tile for any wave of this workgroup
+    }
     if (rt < a.RT) {
         load_x(rt);  // in flight while the B slice is built
     }
 
     // B slice: fragment f = ((s*KS + ks)*NT + ct)*64 + l holds, for lane l,
-    // B[k = s*D + d0 + 32ks + 8(l/16) + e][slot 16ct + l%16], e = 0..7.
-    for (int f = tid; f < NFRAG * 64; f += W * 64) {
-        const int fl = f & 63;
-        const int fr = f >> 6;
-        const int ct = fr % NT;
-        const int sk = fr / NT;
-        const int ks = sk % KS;
-        const int s = sk / KS;
-        bool lo;
-        int j;
-        CL::slot(16 * ct + (fl & 15), lo, j);
-        const int64_t k0 = s * a.D + d0 + 32 * ks + 8 * (fl >> 4);
-        const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + k0);
-        const f32x4_t p0 = src[0], p1 = src[1];
-        float b[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
-        if (a.gamma != nullptr) {
-            const f32x4_t *gs = reinterpret_cast<const f32x4_t *>(a.gamma + k0);
-            const f32x4_t g0 = gs[0], g1 = gs[1];
-            const float gg[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+    // B[k = s*D + d0 + 32ks + 8(l/16) + e][slot 16ct + l%16], e = 0..7.  A
+    // thread builds all NT column tiles of one (s, ks, lane) item, so it reads
+    // the item's gamma once; two items' loads are in flight together.
+    constexpr int ITEMS = N * KS * 64;
+    for (int it0 = tid; it0 < ITEMS; it0 += 2 * W * 64) {
+        f32x4_t ph[2][NT][2];
+        f32x4_t gm[2][2];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                b[e] = b[e] * gg[e];
+        for (int h = 0; h < 2; ++h) {
+            const int it = it0 + h * W * 64;
+            if (it < ITEMS) {
+                const int fl = it & 63;
+                const int sk = it >> 6;
+                const int64_t k0 =
+                    (sk / KS) * a.D + d0 + 32 * (sk % KS) + 8 * (fl >> 4);
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    bool lo;
+                    int j;
+                    CL::slot(16 * ct + (fl & 15), lo, j);
+                    const f32x4_t *src =
+                        reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + k0);
+                    ph[h][ct][0] = src[0];
+                    ph[h][ct][1] = src[1];
+                }
+                if (a.gamma != nullptr) {
+                    const f32x4_t *gs = reinterpret_cast<const f32x4_t *>(a.gamma + k0);
+                    gm[h][0] = gs[0];
+                    gm[h][1] = gs[1];
+                } else {
+                    gm[h][0] = f32x4_t{1.f, 1.f, 1.f, 1.f};
+                    gm[h][1] = f32x4_t{1.f, 1.f, 1.f, 1.f};
+                }
             }
         }
-        float out[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float hi = bf16_bits_to_f32(f32_to_bf16_bits(b[e]));
-            out[e] = lo ? (b[e] - hi) : hi;
+        for (int h = 0; h < 2; ++h) {
+            const int it = it0 + h * W * 64;
+            if (it < ITEMS) {
+                const int fl = it & 63;
+                const int sk = it >> 6;
+#pragma unroll
+                for (int ct = 0; ct < NT; ++ct) {
+                    bool lo;
+                    int j;
+                    CL::slot(16 * ct + (fl & 15), lo, j);
+                    float out[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        float b = ph[h][ct][e >> 2][e & 3];
+                        if (a.gamma != nullptr) {
+                            b = b * gm[h][e >> 2][e & 3];
+                        }
+                        const float hi = bf16_bits_to_f32(f32_to_bf16_bits(b));
+                        out[e] = lo ? (b - hi) : hi;
+                    }
+                    bl[(sk * NT + ct) * 64 + fl] = pack8_bf16(out);
+                }
+            }
         }
-        bl[f] = pack8_bf16(out);
     }
     __syncthreads();
 
@@ -263,86 +336,103 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
         ss = ss + __shfl_xor(ss, 16);
         ss = ss + __shfl_xor(ss, 32);
 
-        // 2. Publish this slice's partials: row 4*grp + i, columns per ColLayout.
-        float *part = a.partial + ((rt * P + p) * 16) * PL::RS;
+        // 2. Publish this slice's partials (C fragment: lane holds rows
+        //    4*grp + i of column slot 16t + rl).
+        float *rec = a.partial + (rt * P + p) * RC::FLOATS;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float *prow = part + (4 * grp + i) * PL::RS;
+            const int r = 4 * grp + i;
 #pragma unroll
             for (int t = 0; t < Q; ++t) {
-                prow[PL::off(16 * t + rl)] = acc[t][i] + acc[Q + t][i];
+                st_dev(rec + RC::col(16 * t + rl) * 16 + r, acc[t][i] + acc[Q + t][i]);
             }
             if constexpr (CL::kHalfTile) {
                 const float other = __shfl_xor(acc[2 * Q][i], 8);
                 if (rl < 8) {
-                    prow[PL::off(16 * Q + rl)] = acc[2 * Q][i] + other;
+                    st_dev(rec + RC::col(16 * Q + rl) * 16 + r, acc[2 * Q][i] + other);
                 }
             }
         }
         if (grp == 0) {
-            part[rl * PL::RS + N] = ss;
+            st_dev(rec + N * 16 + rl, ss);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        wait_all_memory();  // the partials are visible device-wide before we count in
         uint32_t old = 0;
         if (lane == 0) {
-            old = __hip_atomic_fetch_add(a.arrive + rt, 1u, __ATOMIC_RELAXED,
+            old = __hip_atomic_fetch_add(a.arrive + rt * kCounterStride, 1u, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
         }
         old = __shfl(old, 0);
         const int64_t row = rt * 16 + rl;
         const bool rowOk = row < a.T;
 
-        float pre[N];
+        // 3. hPre and invRms of the tile's 16 rows.  Lane (rl, grp) owns hPre
+        //    column grp of row rl.
+        static_assert(N == 4, "the fused path maps the n = 4 hPre columns to the 4 lane groups");
+        const float *tileRec = a.partial + rt * P * RC::FLOATS;
+        float *fin = a.finalPre + rt * RC::FIN;
+        uint32_t *finBits = reinterpret_cast<uint32_t *>(fin);
+        float preC, invRms;
         if (old == (uint32_t)(P - 1)) {
-            // 3a. Last slice in: reduce hPre columns and sumsq over the slices.
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            const float *base = a.partial + (rt * P * 16) * PL::RS;
-            constexpr int NF = N + 1;
-            constexpr int NM = (NF + 3) / 4;
-            float red[NM];
-#pragma unroll
-            for (int m = 0; m < NM; ++m) {
-                const int c = grp + 4 * m;
-                float v = 0.f;
-                if (c < NF) {
-                    const float *src = base + rl * PL::RS + c;
-                    for (int q = 0; q < P; ++q) {
-                        v = v + src[(int64_t)q * 16 * PL::RS];
-                    }
-                }
-                red[m] = v;
-            }
-            float cols[NF];
-#pragma unroll
-            for (int c = 0; c < NF; ++c) {
-                cols[c] = __shfl(red[c >> 2], rl + 16 * (c & 3));
-            }
-            const float invRms = ref_inv_rms(cols[N], a.invFlatDim, a.normEps);
-            const float sP = invRms * alphaPre;
-#pragma unroll
-            for (int s = 0; s < N; ++s) {
-                pre[s] = ref_sigmoid(cols[s] * sP, a.bias[s], a.hcEps);
-            }
+            // Last slice in: sum over the slices (fixed order), evaluate, publish.
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            const float mixC = sum_over_slices(tileRec + grp * 16 + rl, P, RC::FLOATS, true);
+            const float ssum = sum_over_slices(tileRec + N * 16 + rl, P, RC::FLOATS, grp == 0);
+            invRms = ref_inv_rms(__shfl(ssum, rl), a.invFlatDim, a.normEps);
+            preC = ref_sigmoid(mixC * (invRms * alphaPre), a.bias[grp], a.hcEps);
+            __hip_atomic_store(finBits + grp * 16 + rl, __float_as_uint(preC), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
             if (grp == 0) {
-#pragma unroll
-                for (int s = 0; s < N; ++s) {
-                    a.finalPre[(rt * 16 + rl) * N + s] = pre[s];
+                __hip_atomic_store(finBits + N * 16 + rl, __float_as_uint(invRms),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (a.hPre != nullptr && rowOk) {
+                a.hPre[row * N + grp] = preC;
+            }
+        } else {
+            // Poll the published values (the reset kernel filled the block
+            // with a signalling-NaN sentinel that no arithmetic produces).
+            uint32_t spins = 0;
+            uint32_t pb, ib;
+            for (;;) {
+                pb = __hip_atomic_load(finBits + grp * 16 + rl, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                ib = grp == 0 ? __hip_atomic_load(finBits + N * 16 + rl, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : 0u;
+                if (__all(pb != kPreSentinel && ib != kPreSentinel)) {
+                    break;
                 }
+                if (++spins > a.spinLimit) {
+                    if (lane == 0) {
+                        __hip_atomic_store(a.status, kDeviceTimeout, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-            if (lane == 0) {
-                __hip_atomic_store(a.ready + rt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            // 3b. The other columns -> hPost, hRes (off the other slices' path).
+            preC = __uint_as_float(pb);
+            invRms = __shfl(__uint_as_float(ib), rl);
+        }
+        float pre[N];
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+            pre[s] = __shfl(preC, 16 * s + rl);
+        }
+
+        // 3b. hPost / hRes: the M - N other columns in groups of four, group m
+        //     done by slice m mod P (every partial is in: hPre exists).
+        {
+            constexpr int NG = (M - N + 3) / 4;
             const float sQ = invRms * alphaPost;
             const float sR = invRms * alphaRes;
-            for (int jj = N + grp; jj < M; jj += 4) {
-                const float *src = base + rl * PL::RS + PL::off(jj);
-                float v = 0.f;
-                for (int q = 0; q < P; ++q) {
-                    v = v + src[(int64_t)q * 16 * PL::RS];
-                }
-                if (rowOk) {
+            for (int m = p; m < NG; m += P) {
+                const int jj = N + 4 * m + grp;
+                const bool colOk = jj < M;
+                const float v = sum_over_slices(tileRec + RC::col(colOk ? jj : 0) * 16 + rl, P,
+                                                RC::FLOATS, colOk);
+                if (colOk && rowOk) {
                     if (jj < 2 * N) {
                         const float sg = ref_sigmoid(v * sQ, a.bias[jj], 0.0f);
                         a.hPost[row * N + (jj - N)] = sg * 2.0f;
@@ -351,31 +441,6 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
                         a.hRes[row * (N * N) + (jj - 2 * N)] = r + a.bias[jj];
                     }
                 }
-            }
-            if (a.hPre != nullptr && rowOk && grp == 0) {
-#pragma unroll
-                for (int s = 0; s < N; ++s) {
-                    a.hPre[row * N + s] = pre[s];
-                }
-            }
-        } else {
-            // 3c. Wait for the last slice's hPre.
-            if (lane == 0) {
-                uint32_t spins = 0;
-                while (__hip_atomic_load(a.ready + rt, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-                    if (++spins > a.spinLimit) {
-                        __hip_atomic_store(a.status, kDeviceTimeout, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(2);
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-#pragma unroll
-            for (int s = 0; s < N; ++s) {
-                pre[s] = a.finalPre[(rt * 16 + rl) * N + s];
             }
         }
 
@@ -470,7 +535,6 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, hipStream_t stream)
     a.hPre = p.hasHPre ? p.hPre : nullptr;
     a.status = reinterpret_cast<uint32_t *>(ws);
     a.arrive = reinterpret_cast<uint32_t *>(ws + p.wsCounters);
-    a.ready = a.arrive + p.fusedTiles;
     a.finalPre = reinterpret_cast<float *>(ws + p.wsFinal);
     a.partial = reinterpret_cast<float *>(ws + p.wsFusedPartial);
     a.T = p.T;
@@ -482,10 +546,12 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, hipStream_t stream)
     a.normEps = p.normEps;
     a.hcEps = p.hcEps;
     a.invFlatDim = p.invFlatDim;
-    a.spinLimit = 1u << 24;
+    a.spinLimit = 1u << 20;  // about a second of polling per wait
 
-    hipLaunchKernelGGL(fused_reset_kernel, dim3((unsigned)((p.fusedTiles + 255) / 256)), dim3(256),
-                       0, stream, a.arrive, a.ready, (int64_t)p.fusedTiles, a.status);
+    const int64_t finalWords = p.fusedTiles * Rec<N>::FIN;
+    hipLaunchKernelGGL(fused_reset_kernel, dim3((unsigned)((finalWords + 255) / 256)), dim3(256), 0,
+                       stream, a.arrive, reinterpret_cast<uint32_t *>(a.finalPre),
+                       (int64_t)p.fusedTiles, finalWords, a.status);
     err = hipGetLastError();
     if (err != hipSuccess) {
         return err;

@@ -54,9 +54,9 @@ struct Plan {
     // workspace holds one launch at a time.
     size_t wsBsplit = 0;      // split: B fragments
     size_t wsPartial = 0;     // split: [S][T][M+1] partials
-    size_t wsFinal = 0;       // fused: [RT][16][n] hPre
-    size_t wsFusedPartial = 0;// fused: [RT][P][16][RS] partials
-    size_t wsCounters = 0;    // fused: arrival + ready counters, 2 x RT
+    size_t wsFinal = 0;       // fused: per-tile hPre / invRms blocks
+    size_t wsFusedPartial = 0;// fused: per-(tile, slice) exchange records
+    size_t wsCounters = 0;    // fused: per-tile arrival counters
     size_t wsTotal = 0;
 
     // Bound device pointers (caller memory).
@@ -79,11 +79,15 @@ hipError_t launch_fused(const Plan &plan, void *workspace, hipStream_t stream);
 // with numCUs compute units, or -1 if the plan has no fused kernel.
 int fused_max_coresident(const Plan &plan, int numCUs);
 
-// Floats per row of a fused-path partial record for n streams.
-inline int fused_partial_row_floats(int n)
+// Fused-path workspace geometry for n streams (floats): one exchange record
+// per (row tile, slice), one broadcast block per row tile, and one arrival
+// counter per row tile spaced 256 bytes apart.
+inline int fused_record_floats(int n)
 {
     const int M = n * n + 2 * n;
-    return ((n + 1 + 3) / 4) * 4 + ((M - n + 3) / 4) * 4;
+    return ((M + 1 + 1) / 2) * 2 * 16;
 }
+inline int fused_final_floats(int n) { return (((n + 1) * 16 + 31) / 32) * 32; }
+constexpr size_t kFusedCounterBytes = 256;
 
 }  // namespace mhc

@@ -8,8 +8,9 @@ hIn (fp16 / bf16):
   * against the oracle's hIn, at most 1 unit in the last place of the output
     dtype -- except where the sum cancels so far that the (tolerated) fp32
     difference between the device's and the oracle's hPre moves it further.
-    Those elements must still lie within 1 ulp plus sum_s |dhPre[s] * x[s]|,
-    and they must be rare (at most 1 in 10^4).  The GEMM's summation order is
+    Those elements must still lie within 1 ulp + sum_s |dhPre[s] * x[s]| +
+    the fp32 rounding of both n-term sums (2 n 2^-24 sum_s |hPre[s] x[s]|),
+    and they must be rare (at most 1 in 10^3).  The GEMM's summation order is
     hardware-defined in the reference (CANN Cube) and cannot be matched, so
     hPre agrees to fp32 rounding, not bit for bit.
 """
@@ -75,7 +76,7 @@ def _ulp16(bits: np.ndarray, is_bf16: bool) -> np.ndarray:
 
 
 def assert_hin(got_bits, want_bits, x_bits, is_bf16: bool, got_pre, want_pre, orc,
-               max_rare_fraction: float = 1e-4) -> None:
+               max_rare_fraction: float = 1e-3) -> None:
     """hIn check (see the module docstring).  got_pre=None when the device did
     not return hPre: the bound then uses the hPre tolerance instead."""
     got_bits = np.ascontiguousarray(got_bits).view(np.uint16)
@@ -99,7 +100,10 @@ def assert_hin(got_bits, want_bits, x_bits, is_bf16: bool, got_pre, want_pre, or
     far = d > HIN_MAX_ULP
     if far.any():
         xf = np.abs(_decode16(x_bits, is_bf16))                      # [R, n, D]
-        bound = (dpre[:, :, None] * xf).sum(1) * (1 + 1e-6) + _ulp16(want_bits, is_bf16)
+        n = xf.shape[1]
+        wp = np.abs(np.asarray(want_pre, np.float64).reshape(R, -1))
+        arith = 2 * n * 2.0 ** -24 * (wp[:, :, None] * xf).sum(1)
+        bound = (dpre[:, :, None] * xf).sum(1) * (1 + 1e-6) + arith + _ulp16(want_bits, is_bf16)
         diff = np.abs(_decode16(got_bits, is_bf16) - _decode16(want_bits, is_bf16))
         bad = far & (diff > bound)
         if bad.any():
