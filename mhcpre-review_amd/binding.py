@@ -147,7 +147,7 @@ class MhcPreOp:
 
     def __init__(self, x, phi, alpha, bias, gamma=None, norm_eps: float = 1e-6,
                  hc_eps: float = 1e-6, h_in=None, h_post=None, h_res=None, h_pre=None,
-                 phi_dims=None):
+                 phi_dims=None, workspace=None):
         import torch
 
         self.lib = load_library()
@@ -189,8 +189,14 @@ class MhcPreOp:
             raise MhcPreError("mhcPreGetWorkspaceSize", st)
         self.executor = exe
         self.workspace_size = int(ws.value)
-        self.workspace = torch.empty(max(self.workspace_size, 256), dtype=torch.uint8,
-                                     device=dev)
+        if workspace is not None:
+            if workspace.numel() * workspace.element_size() < self.workspace_size:
+                self.close()
+                raise MhcPreError("workspace", STATUS_CODE["MHC_STATUS_WORKSPACE_TOO_SMALL"])
+            self.workspace = workspace
+        else:
+            self.workspace = torch.empty(max(self.workspace_size, 256), dtype=torch.uint8,
+                                         device=dev)
 
     @property
     def path(self) -> str:

@@ -222,3 +222,38 @@ def test_determinism(pkg, device):
     for k in a:
         assert np.array_equal(a[k], b[k]), k
     op.close()
+
+
+def test_shared_workspace_back_to_back(pkg, orc, device):
+    """Two executors with different inputs launched back to back on ONE
+    workspace: nothing from the first launch (exchange records, published
+    hPre, counters) may leak into the second."""
+    import torch
+
+    T, n, D = 400, 4, 7168
+    K, M = n * D, n * n + 2 * n
+    ops, refs, xs = [], [], []
+    ws = None
+    for seed in (11, 12):
+        rng = np.random.default_rng(seed)
+        x = to_bits(rng.standard_normal((T, n, D)).astype(np.float32), True)
+        phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+        alpha = np.full(3, 0.01, dtype=np.float32)
+        bias = rng.uniform(-0.1, 0.1, M).astype(np.float32)
+        gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+        xt, pt, at, bt, gt = to_device(pkg, device, x, True, phi, alpha, bias, gamma)
+        op = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True, workspace=ws)
+        ws = op.workspace
+        ops.append(op)
+        refs.append(orc.mhc_pre(x, True, phi, alpha, bias, gamma))
+        xs.append(x)
+    assert ops[0].path == "fused"
+    for _ in range(2):
+        for op in ops:
+            op.launch()
+        torch.cuda.synchronize()
+        for op, ref, x in zip(ops, refs, xs):
+            assert op.device_status() == 0
+            check(fetch(op), ref, x, True, orc)
+    for op in ops:
+        op.close()
