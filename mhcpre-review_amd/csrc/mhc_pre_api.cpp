@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -24,6 +26,9 @@
 struct mhcPreExecutor {
     mhc::Plan plan;
     int device = -1;  // device the executor was planned on (-1: none visible at plan time)
+    // Epoch of this executor's latest launch; the device status word only
+    // reports a timeout written under it.
+    std::atomic<uint32_t> lastEpoch{0};
 };
 
 namespace {
@@ -74,6 +79,26 @@ int device_cu_count(int &device)
         cache[device] = cus;
     }
     return cache[device];
+}
+
+// Launch epochs: process-wide, strictly increasing from a start that differs
+// between processes (time and address mixed), skipping 0 and ~0 so that a
+// zero- or one-filled workspace can never carry a valid tag.
+uint32_t next_epoch()
+{
+    static std::atomic<uint32_t> counter{[] {
+        const uint64_t t = static_cast<uint64_t>(
+            std::chrono::high_resolution_clock::now().time_since_epoch().count());
+        const uint64_t a = reinterpret_cast<uintptr_t>(&counter);
+        uint64_t h = (t ^ (a << 17)) * 0x9E3779B97F4A7C15ull;
+        return static_cast<uint32_t>(h >> 32);
+    }()};
+    for (;;) {
+        const uint32_t e = counter.fetch_add(1u, std::memory_order_relaxed);
+        if (e != 0u && e != 0xFFFFFFFFu) {
+            return e;
+        }
+    }
 }
 
 // Trailing dims of `t` must be `tail` and its element count `count`.
@@ -207,14 +232,15 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     p.splitS = static_cast<int>(S);
     p.ksPerSlice = static_cast<int>(ksPer);
 
-    // Fused path (n = 4): slices of 32*KS columns, KS preferring 7 (D = 7168
-    // gives 32 slices: 8 XCD-local teams on 256 CUs), then 8, 4, 2, 1.
+    // Fused path (n = 4): slices of DW = 64*KP columns, the widest of 256,
+    // 128, 64 that divides D (a wider slice reads longer runs of each row
+    // and needs fewer exchange records per tile).
     p.fusedTiles = rowTiles;
-    if (n == 4 && (D % 32) == 0) {
-        for (int ks : {7, 8, 4, 2, 1}) {
-            if (D % (32 * ks) == 0) {
-                p.fusedDw = 32 * ks;
-                p.fusedP = static_cast<int>(D / (32 * ks));
+    if (n == 4 && (D % 64) == 0) {
+        for (int kp : {4, 2, 1}) {
+            if (D % (64 * kp) == 0) {
+                p.fusedDw = 64 * kp;
+                p.fusedP = static_cast<int>(D / (64 * kp));
                 break;
             }
         }
@@ -240,10 +266,9 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     if (p.fusedP > 0) {
         p.wsFinal = mhc::kWsHeaderBytes;
         p.wsFusedPartial = align_up(
-            p.wsFinal + static_cast<size_t>(rowTiles) * mhc::fused_final_floats(n) * 4, 256);
-        p.wsCounters = align_up(p.wsFusedPartial + static_cast<size_t>(rowTiles) * p.fusedP *
-                                                        mhc::fused_record_floats(n) * 4, 256);
-        fusedEnd = p.wsCounters + static_cast<size_t>(rowTiles) * mhc::kFusedCounterBytes;
+            p.wsFinal + static_cast<size_t>(rowTiles) * mhc::fused_bcast_words(n) * 8, 256);
+        fusedEnd = align_up(p.wsFusedPartial + static_cast<size_t>(rowTiles) * p.fusedP *
+                                                   mhc::fused_record_words(n) * 8, 256);
     }
     p.wsTotal = std::max(splitEnd, fusedEnd);
     return MHC_STATUS_SUCCESS;
@@ -332,11 +357,14 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
             mhc::Plan lp = p;
             lp.fusedTeams = coresident / p.fusedP;
             lp.fusedGrid = lp.fusedTeams * p.fusedP;
-            err = mhc::launch_fused(lp, workspace, stream);
+            const uint32_t epoch = next_epoch();
+            executor->lastEpoch.store(epoch, std::memory_order_relaxed);
+            err = mhc::launch_fused(lp, workspace, epoch, stream);
             done = true;
         }
     }
     if (!done) {
+        executor->lastEpoch.store(next_epoch(), std::memory_order_relaxed);
         err = mhc::launch_split(p, workspace, stream);
     }
     return err == hipSuccess ? MHC_STATUS_SUCCESS : MHC_STATUS_HIP_ERROR;
@@ -363,11 +391,15 @@ int mhcPreQueryDeviceStatus(void *workspace, uint64_t workspaceSize,
     if (hipStreamSynchronize(stream) != hipSuccess) {
         return MHC_STATUS_HIP_ERROR;
     }
-    uint32_t word = 0;
+    uint64_t word = 0;
     if (hipMemcpy(&word, workspace, sizeof(word), hipMemcpyDeviceToHost) != hipSuccess) {
         return MHC_STATUS_HIP_ERROR;
     }
-    return word == mhc::kDeviceOk ? MHC_STATUS_SUCCESS : MHC_STATUS_DEVICE_TIMEOUT;
+    const uint32_t code = static_cast<uint32_t>(word);
+    const uint32_t epoch = static_cast<uint32_t>(word >> 32);
+    const bool timedOut = code == mhc::kDeviceTimeout &&
+                          epoch == executor->lastEpoch.load(std::memory_order_relaxed);
+    return timedOut ? MHC_STATUS_DEVICE_TIMEOUT : MHC_STATUS_SUCCESS;
 }
 
 const char *mhcPreStatusString(int status)

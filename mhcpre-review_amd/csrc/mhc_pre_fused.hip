@@ -1,34 +1,48 @@
 // Fused MhcPre kernel for gfx950: x is read from HBM once and stays in VGPRs.
 //
-// Work decomposition.  D is cut into P slices of DW = 32*KS columns.  A unit
+// Work decomposition.  D is cut into P slices of DW = 64*KP columns.  A unit
 // is (16-row tile, slice p): the 16 rows x n streams x DW columns of x, held
-// by one wave in VGPRs as the A fragments of v_mfma_f32_16x16x32_bf16.  A
-// workgroup of W waves owns one slice for the whole launch and keeps that
-// slice of the B operand (gamma*phi split into bf16 hi + lo) in LDS.  The P
-// workgroups that own the slices of the same row tiles form a team; teams
-// are XCD-local when the grid is a multiple of 8 (workgroup g runs on XCD
-// g % 8 and team = g % numTeams).
+// by one wave in VGPRs.  A workgroup of W = 8 waves (two per SIMD) owns one
+// slice for the whole launch and keeps that slice of the B operand
+// (gamma*phi split into bf16 hi + lo) in LDS.  The P workgroups that own the
+// slices of the same row tiles form a team (team = workgroup % numTeams).
+//
+// Register layout of x.  A unit is loaded as whole 128-byte lines: register
+// (s, kp, h) holds, in lane l, row 8h + (l & 7) and the 8 columns starting at
+// 64kp + 8(l >> 4) + 32((l >> 3) & 1) of stream s, so the 8 lanes of a row
+// read (and later write, for hIn) one full line.  The MFMA A operand wants
+// lane l to hold row l & 15; one DPP row_ror:8 move with a bank mask per
+// dword turns registers (kp, h = 0, 1) into the A fragments of k-steps 2kp
+// and 2kp + 1.  x is read and hIn written with nontemporal buffer accesses.
 //
 // Per unit a wave:
 //   1. multiplies its x block by the LDS B slice (MFMA, fp32 accumulate) and
-//      sums x^2 from the same registers;
-//   2. publishes the slice's partial sums (M mix columns + sumsq per row) and
-//      counts itself in on the row tile's arrival counter;
-//   3. the last of the P slices to arrive sums the hPre columns and sumsq
-//      over all slices in a fixed order, evaluates invRms and hPre and
-//      publishes hPre; then it sums the remaining columns and writes hPost /
-//      hRes (and hPre when asked); every other slice polls the published hPre
-//      of its rows;
-//   4. computes hIn for its DW columns from the x still in its registers.
-// The last-arriver rule needs no wave to wait for one that has not arrived,
-// and the cooperative launch keeps every workgroup resident, so the waits
-// always end; each is still bounded by a spin limit that records
-// kDeviceTimeout in the status word instead of hanging.
+//      forms the Gram matrix of its rows with the same fragments, whose
+//      diagonal is the slice's sum of squares per row;
+//   2. publishes the slice's partial sums (M mix columns + sumsq per row) as
+//      tagged words (below) and, without waiting, finishes the hPost / hRes
+//      columns it owns for its previous tile;
+//   3. obtains hPre and invRms of its 16 rows: the tile's reducer (slice
+//      tile mod P) polls the P records until every word carries this launch's
+//      tag, sums the hPre columns and sumsq over the slices in a fixed order,
+//      evaluates invRms and hPre and publishes them as tagged words; every
+//      other slice polls that block;
+//   4. computes hIn for its DW columns from the x still in its registers and,
+//      as each register group is consumed, issues the loads of its next unit
+//      into it.
 //
-// Exchange memory is accessed with device-scope (sc1) loads and stores, and a
-// wave waits for its stores to complete (s_waitcnt) before the atomic that
-// announces them; no agent-scope fence is used, because on a multi-L2 device
-// each one writes back or invalidates a whole L2.
+// Exchange words.  Every exchanged value is one 8-byte word: the fp32 bits in
+// the low half and a tag in the high half, written and read as single-copy
+// atomic 64-bit accesses at device scope (sc1).  The tag is a hash of the
+// word's position mixed with a per-launch epoch, so a word holds the current
+// value exactly when its tag matches: no arrival counter, no release wait and
+// no reset of the workspace between launches.  A reader accepts a block only
+// when every word it read carries the expected tag; a block left over from an
+// earlier launch (another epoch) or filled with any constant never does.
+// Every wait is bounded by a spin limit; running out records kDeviceTimeout
+// with the launch's epoch in the status word instead of hanging.  The
+// cooperative launch keeps every workgroup resident, so a reducer is never
+// waiting on a workgroup that has not started.
 
 #include "mhc_pre_device.h"
 #include "mhc_pre_internal.h"
@@ -43,7 +57,7 @@ namespace {
 
 using namespace dev;
 
-constexpr int kFusedWaves = 8;  // waves per workgroup (2 per SIMD)
+constexpr int kFusedWaves = 8;  // waves per workgroup (two per SIMD)
 
 struct FusedArgs {
     const uint16_t *x;
@@ -55,10 +69,9 @@ struct FusedArgs {
     float *hPost;
     float *hRes;
     float *hPre;
-    float *partial;      // [RT][P] records of Rec<N>::FLOATS
-    float *finalPre;     // [RT] blocks of Rec<N>::FIN
-    uint32_t *arrive;    // [RT] counters, kCounterStride words apart
-    uint32_t *status;
+    uint64_t *recs;      // [RT][P] records of Rec<N>::WORDS tagged words
+    uint64_t *bcast;     // [RT] blocks of Rec<N>::BWORDS tagged words
+    uint64_t *status;    // (epoch << 32) | kDeviceTimeout after a timeout
     int64_t T;
     int64_t D;
     int64_t K;
@@ -68,6 +81,7 @@ struct FusedArgs {
     float normEps;
     float hcEps;
     float invFlatDim;
+    uint32_t epoch;
     uint32_t spinLimit;
 };
 
@@ -99,68 +113,133 @@ struct ColLayout {
 };
 
 // Exchange record of one (row tile, slice), column-major: column c holds its
-// 16 rows contiguously (64 bytes).  Column N is the sum of squares; mix column
-// j sits at column j (j < N, the hPre columns) or j + 1.  The column count is
-// even, so a record is a whole number of 128-byte lines and no line is
-// written by two slices.  A wave reads four columns of 16 rows -- one 256-byte
-// span -- per load instruction.
+// 16 rows as 16 consecutive tagged words (128 bytes).  Column N is the sum of
+// squares; mix column j sits at column j (j < N, the hPre columns) or j + 1.
+// The per-tile broadcast block holds hPre columns 0..N-1 and invRms at
+// column N, 16 rows each.
 template <int N>
 struct Rec {
     static constexpr int M = N * N + 2 * N;
-    static constexpr int RC = ((M + 1 + 1) / 2) * 2;
-    static constexpr int FLOATS = RC * 16;
-    // Per-tile broadcast block written by the last slice: hPre columns
-    // 0..N-1 and invRms at column N, 16 rows each, padded to 128-byte lines.
-    static constexpr int FIN = (((N + 1) * 16 + 31) / 32) * 32;
+    static constexpr int COLS = M + 1;
+    static constexpr int WORDS = COLS * 16;
+    static constexpr int BWORDS = (N + 1) * 16;
     __device__ static int col(int j) { return j < N ? j : j + 1; }
 };
 
-// Arrival counters are spaced one 256-byte line apart: device-scope atomics
-// on one line serialize, and the tiles' counters are hit concurrently.
-constexpr int kCounterStride = 64;  // uint32 words
-
-// hPre slots not yet written hold this signalling-NaN pattern; arithmetic
-// only ever produces quiet NaNs, so a computed hPre can never equal it.
-constexpr uint32_t kPreSentinel = 0x7F80DEADu;
-
-// Sum over slices q = 0..P-1, in that order, of the float at src + q*step;
-// loads are issued 32 slices at a time so they are in flight together.
-__device__ __forceinline__ float sum_over_slices(const float *src, int P, int step, bool active)
+// Tags: a multiplicative hash of the word's position (distinct for the
+// records and the broadcast blocks) mixed with the launch epoch.
+__device__ __forceinline__ uint32_t rec_tag(uint32_t pos, uint32_t epoch)
 {
-    float v = 0.f;
-    for (int q0 = 0; q0 < P; q0 += 32) {
-        float t[32];
-#pragma unroll
-        for (int u = 0; u < 32; ++u) {
-            const int q = q0 + u;
-            t[u] = (active && q < P) ? ld_dev(src + (int64_t)q * step) : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < 32; ++u) {
-            v = v + t[u];
-        }
-    }
-    return v;
+    return (pos * 0x9E3779B1u) ^ epoch;
+}
+__device__ __forceinline__ uint32_t bcast_tag(uint32_t pos, uint32_t epoch)
+{
+    return (pos * 0x85EBCA77u) ^ epoch ^ 0xC2B2AE3Du;
 }
 
-__global__ __launch_bounds__(256) void fused_reset_kernel(uint32_t *__restrict__ arrive,
-                                                          uint32_t *__restrict__ finalPre,
-                                                          int64_t RT, int64_t finalWords,
-                                                          uint32_t *__restrict__ status)
+__device__ __forceinline__ void st_word(uint64_t *p, float v, uint32_t tag)
 {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < RT) {
-        arrive[i * kCounterStride] = 0u;
+    __hip_atomic_store(p, (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t ld_word(const uint64_t *p)
+{
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Cache-policy operands of the buffer builtins.
+constexpr int kCpolNt = 2;    // nontemporal: x and hIn are streamed once
+constexpr int kCpolDev = 16;  // sc1: device-scope coherent
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, 0x00020000);
+}
+
+// Sums over the P slice records of a tile, for record columns c0 .. c0+NC-1
+// and all 16 rows, checking every word's tag.  Lane l takes item
+// it = l % (8 NC) (column c0 + it/8, rows 2(it%8) and 2(it%8) + 1, one 16-byte
+// load per slice) and slice group sg = l / (8 NC), and adds slices sg,
+// sg + NSG, ... in increasing order; the groups are then added in order
+// 0, 1, ..., NSG-1, so the result is a fixed-order sum.  Loads are issued U
+// slices per lane at a time.  Lanes it < 8 NC return the two row totals of
+// their item; valid is true when every word read carried the expected tag.
+template <int NC, int COLS, int U>
+__device__ __forceinline__ float2 sum_records(__amdgpu_buffer_rsrc_t r, int c0, int P, int lane,
+                                              uint32_t tileBase, uint32_t epoch, bool &valid)
+{
+    constexpr int NIT = 8 * NC;
+    constexpr int NSG = 64 / NIT;
+    static_assert(NSG >= 1, "at most 8 columns per call");
+    const int it = lane % NIT;
+    const int sg = lane / NIT;
+    const bool act = sg < NSG;
+    const int c = c0 + it / 8;
+    const int row0 = 2 * (it % 8);
+    float2 acc = make_float2(0.f, 0.f);
+    bool ok = true;
+    for (int q0 = 0; q0 < P; q0 += NSG * U) {
+        u32x4_t t[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = q0 + sg + NSG * u;
+            t[u] = (act && q < P)
+                       ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         r, ((q * COLS + c) * 16 + row0) * 8, 0,
+                                                         kCpolDev))
+                       : u32x4_t{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = q0 + sg + NSG * u;
+            if (act && q < P) {
+                const uint32_t pos = tileBase + (uint32_t)((q * COLS + c) * 16 + row0);
+                ok = ok && t[u][1] == rec_tag(pos, epoch) && t[u][3] == rec_tag(pos + 1u, epoch);
+                acc.x = acc.x + __uint_as_float(t[u][0]);
+                acc.y = acc.y + __uint_as_float(t[u][2]);
+            }
+        }
     }
-    if (i < finalWords) {
-        finalPre[i] = kPreSentinel;
+    float2 tot = acc;
+#pragma unroll
+    for (int k = 1; k < NSG; ++k) {
+        tot.x = tot.x + __shfl(acc.x, it + k * NIT);
+        tot.y = tot.y + __shfl(acc.y, it + k * NIT);
     }
-    if (i == 0) {
-        *status = kDeviceOk;
+    valid = __all(ok);
+    return tot;
+}
+
+// A fragments of k-steps 2kp and 2kp + 1 from the line-layout registers r0
+// (rows 0-7) and r1 (rows 8-15): lanes with bit 3 set take the other
+// register's lane l ^ 8 (DPP row_ror:8 with banks 2-3 or 0-1 enabled).
+__device__ __forceinline__ void lines_to_frags(const u32x4_t &r0, const u32x4_t &r1, u32x4_t &k0,
+                                               u32x4_t &k1)
+{
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        k0[w] = (uint32_t)__builtin_amdgcn_update_dpp((int)r0[w], (int)r1[w], 0x128, 0xF, 0xC, false);
+        k1[w] = (uint32_t)__builtin_amdgcn_update_dpp((int)r1[w], (int)r0[w], 0x128, 0xF, 0x3, false);
     }
 }
 
-template <int N, int KS, bool kBf16>
+__device__ __forceinline__ f32x4_t mfma16_f16(const u32x4_t &a, const u32x4_t &b, const f32x4_t &c)
+{
+    typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void record_timeout(const FusedArgs &a, int lane)
+{
+    if (lane == 0) {
+        __hip_atomic_store(a.status, ((uint64_t)a.epoch << 32) | kDeviceTimeout, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int N, int KP, bool kBf16>
 __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
 {
     using S = Shape<N>;
@@ -169,9 +248,11 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     using CL = ColLayout<M>;
     using RC = Rec<N>;
     constexpr int W = kFusedWaves;
-    constexpr int DW = 32 * KS;
+    constexpr int KS = 2 * KP;  // 32-column MFMA k-steps per stream
+    constexpr int DW = 64 * KP;
     constexpr int Q = CL::Q;
-    extern __shared__ u32x4_t bl[];  // [NFRAG][64] B fragments of this workgroup's slice
+    extern __shared__ u32x4_t bl[];  // [N*KS][NT][64] B fragments, then per-wave scratch
+    static_assert(N == 4, "the fused path maps the n = 4 hPre columns to the 4 lane groups");
 
     const int P = a.P;
     const int numTeams = a.numTeams;
@@ -184,31 +265,41 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int grp = lane >> 4;
-    const int rl = lane & 15;
     const int64_t d0 = (int64_t)p * DW;
     const int64_t stride = (int64_t)numTeams * W;
+    float *scratch = reinterpret_cast<float *>(bl + N * KS * NT * 64) + wave * RC::BWORDS;
     int64_t rt = (int64_t)team * W + wave;
 
-    u32x4_t xr[N][KS];
-    auto load_x = [&](int64_t rtile) {
-        const int64_t row = rtile * 16 + rl;
-        const bool ok = row < a.T;
-        const uint16_t *base = a.x + (ok ? row : 0) * a.K + d0 + 8 * grp;
-#pragma unroll
-        for (int s = 0; s < N; ++s) {
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                xr[s][ks] = ok ? *reinterpret_cast<const u32x4_t *>(base + s * a.D + 32 * ks)
-                               : u32x4_t{0u, 0u, 0u, 0u};
-            }
-        }
+    u32x4_t xr[N][KP][2];
+    // x and hIn of a tile go through buffer resources based at the tile's
+    // first row and sized to its valid rows: loads past T read zero and
+    // stores past T are dropped.
+    auto tile_rows = [&](int64_t rtile) { return (int)min((int64_t)16, a.T - rtile * 16); };
+    auto load_line = [&](__amdgpu_buffer_rsrc_t xrs, int xLane, int Ki, int Di, int d0i, int s,
+                         int kp, int h) {
+        const int so = (8 * h * Ki + s * Di + d0i) * 2;
+        xr[s][kp][h] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xLane + 128 * kp, so, kCpolNt));
     };
     if ((int64_t)team * W >= a.RT) {
         return;  // no row tile for any wave of this workgroup
     }
     if (rt < a.RT) {
-        load_x(rt);  // in flight while the B slice is built
+        // In flight while the B slice is built.
+        const int lrow = lane & 7;
+        const int lineOff = 8 * (lane >> 4) + 32 * ((lane >> 3) & 1);
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + rt * 16 * a.K, tile_rows(rt) * (int)a.K * 2);
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+#pragma unroll
+            for (int kp = 0; kp < KP; ++kp) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    load_line(xrs, (lrow * (int)a.K + lineOff) * 2, (int)a.K, (int)a.D, (int)d0, s,
+                              kp, h);
+                }
+            }
+        }
     }
 
     // B slice: fragment f = ((s*KS + ks)*NT + ct)*64 + l holds, for lane l,
@@ -278,44 +369,112 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     const float alphaPre = a.alpha[0];
     const float alphaPost = a.alpha[1];
     const float alphaRes = a.alpha[2];
+    const uint32_t epoch = a.epoch;
 
+    // hPost / hRes columns (mix columns N .. M-1) of a finished tile: column
+    // N + m is done by slice m mod P, from the records (every one of them is
+    // complete once the tile's hPre exists, but the tags are checked anyway).
+    auto post_res = [&](int64_t rtile, float invRmsLane, int Pi, int laneO) {
+        const __amdgpu_buffer_rsrc_t tr =
+            make_rsrc(a.recs + rtile * Pi * RC::WORDS, Pi * RC::WORDS * 8);
+        const uint32_t tileBase = (uint32_t)(rtile * Pi * RC::WORDS);
+        for (int m = p; m < M - N; m += Pi) {
+            const int jj = N + m;
+            float2 tot;
+            bool valid = false;
+            for (uint32_t spins = 0;; ++spins) {
+                tot = sum_records<1, RC::COLS, 4>(tr, RC::col(jj), Pi, laneO, tileBase, epoch, valid);
+                if (valid) {
+                    break;
+                }
+                if (spins >= a.spinLimit) {
+                    record_timeout(a, laneO);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            const int r0 = 2 * (laneO % 8);
+            const float ir0 = __shfl(invRmsLane, r0);
+            const float ir1 = __shfl(invRmsLane, r0 + 1);
+            if (laneO < 8) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int64_t row = rtile * 16 + r0 + e;
+                    const float v = e == 0 ? tot.x : tot.y;
+                    const float ir = e == 0 ? ir0 : ir1;
+                    if (row < a.T) {
+                        if (jj < 2 * N) {
+                            const float sg = ref_sigmoid(v * (ir * alphaPost), a.bias[jj], 0.0f);
+                            a.hPost[row * N + (jj - N)] = sg * 2.0f;
+                        } else {
+                            const float r = v * (ir * alphaRes);
+                            a.hRes[row * (N * N) + (jj - 2 * N)] = r + a.bias[jj];
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    int64_t prevTile = -1;
+    float prevInvRms = 0.f;
     for (; rt < a.RT; rt += stride) {
-        // 1. GEMM slice + sum of squares.
+        // Per-unit copies the compiler cannot see through: the offsets
+        // derived from them are recomputed each unit (a few instructions)
+        // instead of being hoisted out of the loop and held in registers.
+        int laneO = lane;
+        int Ki = (int)a.K;
+        int Di = (int)a.D;
+        int d0i = (int)d0;
+        int Pi = P;
+        asm volatile("" : "+v"(laneO), "+s"(Ki), "+s"(Di), "+s"(d0i), "+s"(Pi));
+        const int grp = laneO >> 4;
+        const int rl = laneO & 15;
+        const int lrow = laneO & 7;
+        const int lineOff = 8 * (laneO >> 4) + 32 * ((laneO >> 3) & 1);
+
+        // 1. GEMM slice + Gram matrix (sum of squares on its diagonal).  The
+        //    B fragments of the next k-step are read while this step's MFMAs
+        //    run; the compiler barriers keep the scheduler from hoisting more.
         f32x4_t acc[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
-        float ss = 0.f;
-        // B fragments are read one k-step ahead of the MFMAs that use them;
-        // the compiler barriers stop the scheduler from hoisting more reads
-        // (the x block already holds most of the VGPRs).
+        f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
         constexpr int STEPS = N * KS;
         u32x4_t bcur[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            bcur[t] = bl[t * 64 + lane];
+            bcur[t] = bl[t * 64 + laneO];
         }
+        u32x4_t kf[2];
 #pragma unroll
         for (int st = 0; st < STEPS; ++st) {
+            const int s = st / KS;
+            const int kp = (st % KS) >> 1;
+            const int q = st & 1;
             u32x4_t bnext[NT];
             if (st + 1 < STEPS) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    bnext[t] = bl[((st + 1) * NT + t) * 64 + lane];
+                    bnext[t] = bl[((st + 1) * NT + t) * 64 + laneO];
                 }
             }
             asm volatile("" ::: "memory");
-            const u32x4_t av = xr[st / KS][st % KS];
-            ss = sumsq8<kBf16>(av, ss);
+            if (q == 0) {
+                lines_to_frags(xr[s][kp][0], xr[s][kp][1], kf[0], kf[1]);
+            }
             if constexpr (kBf16) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    acc[t] = mfma16(av, bcur[t], acc[t]);
+                    acc[t] = mfma16(kf[q], bcur[t], acc[t]);
                 }
+                gram = mfma16(kf[q], kf[q], gram);
             } else {
+                gram = mfma16_f16(kf[q], kf[q], gram);
                 float f[8];
-                unpack8<kBf16>(av, f);
+                unpack8<kBf16>(kf[q], f);
                 u32x4_t ahi, alo;
                 split_f16_to_bf16(f, ahi, alo);
 #pragma unroll
@@ -332,193 +491,219 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
                     bcur[t] = bnext[t];
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        ss = ss + __shfl_xor(ss, 16);
-        ss = ss + __shfl_xor(ss, 32);
+        // Gram diagonal: row r sits in lane 16(r/4) + r, register r % 4.
+        const bool diagLane = (rl >> 2) == grp;
+        const int di = rl & 3;
+        const float ss = di == 0 ? gram[0] : di == 1 ? gram[1] : di == 2 ? gram[2] : gram[3];
 
-        // 2. Publish this slice's partials (C fragment: lane holds rows
-        //    4*grp + i of column slot 16t + rl).
-        float *rec = a.partial + (rt * P + p) * RC::FLOATS;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 4 * grp + i;
-#pragma unroll
-            for (int t = 0; t < Q; ++t) {
-                st_dev(rec + RC::col(16 * t + rl) * 16 + r, acc[t][i] + acc[Q + t][i]);
-            }
-            if constexpr (CL::kHalfTile) {
-                const float other = __shfl_xor(acc[2 * Q][i], 8);
-                if (rl < 8) {
-                    st_dev(rec + RC::col(16 * Q + rl) * 16 + r, acc[2 * Q][i] + other);
-                }
-            }
-        }
-        if (grp == 0) {
-            st_dev(rec + N * 16 + rl, ss);
-        }
-        wait_all_memory();  // the partials are visible device-wide before we count in
-        uint32_t old = 0;
-        if (lane == 0) {
-            old = __hip_atomic_fetch_add(a.arrive + rt * kCounterStride, 1u, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-        }
-        old = __shfl(old, 0);
-        const int64_t row = rt * 16 + rl;
-        const bool rowOk = row < a.T;
-
-        // 3. hPre and invRms of the tile's 16 rows.  Lane (rl, grp) owns hPre
-        //    column grp of row rl.
-        static_assert(N == 4, "the fused path maps the n = 4 hPre columns to the 4 lane groups");
-        const float *tileRec = a.partial + rt * P * RC::FLOATS;
-        float *fin = a.finalPre + rt * RC::FIN;
-        uint32_t *finBits = reinterpret_cast<uint32_t *>(fin);
-        float preC, invRms;
-        if (old == (uint32_t)(P - 1)) {
-            // Last slice in: sum over the slices (fixed order), evaluate, publish.
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            const float mixC = sum_over_slices(tileRec + grp * 16 + rl, P, RC::FLOATS, true);
-            const float ssum = sum_over_slices(tileRec + N * 16 + rl, P, RC::FLOATS, grp == 0);
-            invRms = ref_inv_rms(__shfl(ssum, rl), a.invFlatDim, a.normEps);
-            preC = ref_sigmoid(mixC * (invRms * alphaPre), a.bias[grp], a.hcEps);
-            __hip_atomic_store(finBits + grp * 16 + rl, __float_as_uint(preC), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            if (grp == 0) {
-                __hip_atomic_store(finBits + N * 16 + rl, __float_as_uint(invRms),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            if (a.hPre != nullptr && rowOk) {
-                a.hPre[row * N + grp] = preC;
-            }
-        } else {
-            // Poll the published values (the reset kernel filled the block
-            // with a signalling-NaN sentinel that no arithmetic produces).
-            uint32_t spins = 0;
-            uint32_t pb, ib;
-            for (;;) {
-                pb = __hip_atomic_load(finBits + grp * 16 + rl, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                ib = grp == 0 ? __hip_atomic_load(finBits + N * 16 + rl, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT)
-                              : 0u;
-                if (__all(pb != kPreSentinel && ib != kPreSentinel)) {
-                    break;
-                }
-                if (++spins > a.spinLimit) {
-                    if (lane == 0) {
-                        __hip_atomic_store(a.status, kDeviceTimeout, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-            }
-            preC = __uint_as_float(pb);
-            invRms = __shfl(__uint_as_float(ib), rl);
-        }
-        float pre[N];
-#pragma unroll
-        for (int s = 0; s < N; ++s) {
-            pre[s] = __shfl(preC, 16 * s + rl);
-        }
-
-        // 3b. hPost / hRes: the M - N other columns in groups of four, group m
-        //     done by slice m mod P (every partial is in: hPre exists).
+        // 2. Publish this slice's partials as tagged words (C fragment: lane
+        //    holds rows 4*grp + i of column slot 16t + rl).
         {
-            constexpr int NG = (M - N + 3) / 4;
-            const float sQ = invRms * alphaPost;
-            const float sR = invRms * alphaRes;
-            for (int m = p; m < NG; m += P) {
-                const int jj = N + 4 * m + grp;
-                const bool colOk = jj < M;
-                const float v = sum_over_slices(tileRec + RC::col(colOk ? jj : 0) * 16 + rl, P,
-                                                RC::FLOATS, colOk);
-                if (colOk && rowOk) {
-                    if (jj < 2 * N) {
-                        const float sg = ref_sigmoid(v * sQ, a.bias[jj], 0.0f);
-                        a.hPost[row * N + (jj - N)] = sg * 2.0f;
-                    } else {
-                        const float r = v * sR;
-                        a.hRes[row * (N * N) + (jj - 2 * N)] = r + a.bias[jj];
+            const uint32_t recBase = (uint32_t)((rt * Pi + p) * RC::WORDS);
+            uint64_t *rec = a.recs + (rt * Pi + p) * RC::WORDS;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * grp + i;
+#pragma unroll
+                for (int t = 0; t < Q; ++t) {
+                    const int w = RC::col(16 * t + rl) * 16 + r;
+                    st_word(rec + w, acc[t][i] + acc[Q + t][i], rec_tag(recBase + w, epoch));
+                }
+                if constexpr (CL::kHalfTile) {
+                    const float other = __shfl_xor(acc[2 * Q][i], 8);
+                    if (rl < 8) {
+                        const int w = RC::col(16 * Q + rl) * 16 + r;
+                        st_word(rec + w, acc[2 * Q][i] + other, rec_tag(recBase + w, epoch));
                     }
                 }
             }
+            if (diagLane) {
+                const int w = N * 16 + rl;
+                st_word(rec + w, ss, rec_tag(recBase + w, epoch));
+            }
+        }
+        // The previous tile's hPost / hRes fill the time the other slices
+        // need to publish.
+        if (prevTile >= 0) {
+            post_res(prevTile, prevInvRms, Pi, laneO);
         }
 
-        // 4. hIn for this slice's columns from the registers.
-        if (rowOk) {
-            uint16_t *out = a.hIn + row * a.D + d0 + 8 * grp;
+        // 3. hPre and invRms of the tile's 16 rows: lane (rl, grp) ends with
+        //    hPre column grp and invRms of row rl.
+        uint64_t *blk = a.bcast + rt * RC::BWORDS;
+        const uint32_t blkBase = (uint32_t)(rt * RC::BWORDS);
+        float preC, invRms;
+        if (rt % Pi == p) {
+            // Reducer: sum columns 0..N (hPre mix columns, sum of squares)
+            // over the slices in a fixed order once every record is in.
+            const __amdgpu_buffer_rsrc_t tr = make_rsrc(a.recs + rt * Pi * RC::WORDS, Pi * RC::WORDS * 8);
+            const uint32_t tileBase = (uint32_t)(rt * Pi * RC::WORDS);
+            float2 tot;
+            bool valid = false;
+            for (uint32_t spins = 0;; ++spins) {
+                tot = sum_records<N + 1, RC::COLS, 14>(tr, 0, Pi, laneO, tileBase, epoch, valid);
+                if (valid) {
+                    break;
+                }
+                if (spins >= a.spinLimit) {
+                    record_timeout(a, laneO);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            constexpr int NIT = 8 * (N + 1);
+            const int it = laneO % NIT;
+            const int c = it / 8;
+            const int r0 = 2 * (it % 8);
+            // invRms of rows r0, r0 + 1 from the sum-of-squares lanes (c == N).
+            float ir0 = ref_inv_rms(tot.x, a.invFlatDim, a.normEps);
+            float ir1 = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
+            ir0 = __shfl(ir0, 8 * N + it % 8);
+            ir1 = __shfl(ir1, 8 * N + it % 8);
+            if (laneO < NIT) {
+                const float bc = c < N ? a.bias[c] : 0.f;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                // Unpack one k-step at a time (an empty asm that "rewrites"
-                // the registers keeps the unpacking from being hoisted).
+                for (int e = 0; e < 2; ++e) {
+                    const float ir = e == 0 ? ir0 : ir1;
+                    const float mix = e == 0 ? tot.x : tot.y;
+                    const float v = c < N ? ref_sigmoid(mix * (ir * alphaPre), bc, a.hcEps) : ir;
+                    const int idx = c * 16 + r0 + e;
+                    scratch[idx] = v;
+                    st_word(blk + idx, v, bcast_tag(blkBase + idx, epoch));
+                    const int64_t row = rt * 16 + r0 + e;
+                    if (c < N && a.hPre != nullptr && row < a.T) {
+                        a.hPre[row * N + c] = v;
+                    }
+                }
+            }
+            preC = scratch[grp * 16 + rl];
+            invRms = scratch[N * 16 + rl];
+        } else {
+            uint64_t pw = 0, iw = 0;
+            for (uint32_t spins = 0;; ++spins) {
+                pw = ld_word(blk + grp * 16 + rl);
+                iw = ld_word(blk + N * 16 + rl);
+                const bool ok = (uint32_t)(pw >> 32) == bcast_tag(blkBase + grp * 16 + rl, epoch) &&
+                                (uint32_t)(iw >> 32) == bcast_tag(blkBase + N * 16 + rl, epoch);
+                if (__all(ok)) {
+                    break;
+                }
+                if (spins >= a.spinLimit) {
+                    record_timeout(a, laneO);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            preC = __uint_as_float((uint32_t)pw);
+            invRms = __uint_as_float((uint32_t)iw);
+        }
+        prevTile = rt;
+        prevInvRms = invRms;
+
+        // hPre of the two line-layout rows of this lane: 8h + (lane & 7).
+        float pre[2][N];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int s = 0; s < N; ++s) {
+                pre[h][s] = __shfl(preC, 16 * s + 8 * h + lrow);
+            }
+        }
+
+        // 4. hIn for this slice's columns from the registers; each consumed
+        //    register group is refilled with the next unit's x at once.
+        const int64_t rtNext = rt + stride;
+        const bool more = rtNext < a.RT;
+        const __amdgpu_buffer_rsrc_t hrs = make_rsrc(a.hIn + rt * 16 * a.D, tile_rows(rt) * Di * 2);
+        const __amdgpu_buffer_rsrc_t xrs =
+            make_rsrc(a.x + (more ? rtNext : rt) * 16 * a.K, tile_rows(more ? rtNext : rt) * Ki * 2);
+        const int hLane = (lrow * Di + lineOff) * 2;
+        const int xLane = (lrow * Ki + lineOff) * 2;
+#pragma unroll
+        for (int kp = 0; kp < KP; ++kp) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                // An empty asm that "rewrites" the registers keeps the
+                // unpacking from being hoisted ahead of this group.
 #pragma unroll
                 for (int s = 0; s < N; ++s) {
-                    asm volatile("" : "+v"(xr[s][ks]));
+                    asm volatile("" : "+v"(xr[s][kp][h]));
                 }
-                float h[8];
+                float hv[8];
 #pragma unroll
                 for (int s = 0; s < N; ++s) {
                     float f[8];
-                    unpack8<kBf16>(xr[s][ks], f);
+                    unpack8<kBf16>(xr[s][kp][h], f);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const float prod = pre[s] * f[e];
-                        h[e] = (s == 0) ? prod : h[e] + prod;
+                        const float prod = pre[h][s] * f[e];
+                        hv[e] = (s == 0) ? prod : hv[e] + prod;
                     }
                 }
                 u32x4_t o;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
-                    o[w] = f32_to_x<kBf16>(h[2 * w]) | (f32_to_x<kBf16>(h[2 * w + 1]) << 16);
+                    o[w] = f32_to_x<kBf16>(hv[2 * w]) | (f32_to_x<kBf16>(hv[2 * w + 1]) << 16);
                 }
-                *reinterpret_cast<u32x4_t *>(out + 32 * ks) = o;
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, o), hrs,
+                    hLane + 128 * kp, (8 * h * Di + d0i) * 2, kCpolNt);
+                if (more) {
+#pragma unroll
+                    for (int s = 0; s < N; ++s) {
+                        load_line(xrs, xLane, Ki, Di, d0i, s, kp, h);
+                    }
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (rt + stride < a.RT) {
-            load_x(rt + stride);
-        }
+    }
+    if (prevTile >= 0) {
+        post_res(prevTile, prevInvRms, P, lane);
     }
 }
 
-template <int N, int KS, bool kBf16>
+template <int N, int KP, bool kBf16>
 size_t fused_lds_bytes()
 {
-    return (size_t)N * KS * Shape<N>::NT * 64 * sizeof(u32x4_t);
+    return (size_t)N * 2 * KP * Shape<N>::NT * 64 * sizeof(u32x4_t) +
+           (size_t)kFusedWaves * Rec<N>::BWORDS * sizeof(float);
 }
 
-template <int N, int KS, bool kBf16>
+template <int N, int KP, bool kBf16>
 hipError_t fused_prepare_attr()
 {
     static std::once_flag once;
     static hipError_t err = hipSuccess;
     std::call_once(once, [] {
-        err = hipFuncSetAttribute(reinterpret_cast<const void *>(&fused_kernel<N, KS, kBf16>),
+        err = hipFuncSetAttribute(reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)fused_lds_bytes<N, KS, kBf16>());
+                                  (int)fused_lds_bytes<N, KP, kBf16>());
     });
     return err;
 }
 
-template <int N, int KS, bool kBf16>
+template <int N, int KP, bool kBf16>
 int fused_coresident_t(int numCUs)
 {
-    if (fused_prepare_attr<N, KS, kBf16>() != hipSuccess) {
+    if (fused_prepare_attr<N, KP, kBf16>() != hipSuccess) {
         return -1;
     }
     int perCU = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &perCU, reinterpret_cast<const void *>(&fused_kernel<N, KS, kBf16>),
-            kFusedWaves * 64, fused_lds_bytes<N, KS, kBf16>()) != hipSuccess) {
+            &perCU, reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16>),
+            kFusedWaves * 64, fused_lds_bytes<N, KP, kBf16>()) != hipSuccess) {
         return -1;
     }
     return perCU * numCUs;
 }
 
-template <int N, int KS, bool kBf16>
-hipError_t launch_fused_t(const Plan &p, void *workspace, hipStream_t stream)
+template <int N, int KP, bool kBf16>
+hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t epoch, hipStream_t stream)
 {
-    hipError_t err = fused_prepare_attr<N, KS, kBf16>();
+    hipError_t err = fused_prepare_attr<N, KP, kBf16>();
     if (err != hipSuccess) {
         return err;
     }
@@ -533,10 +718,9 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, hipStream_t stream)
     a.hPost = p.hPost;
     a.hRes = p.hRes;
     a.hPre = p.hasHPre ? p.hPre : nullptr;
-    a.status = reinterpret_cast<uint32_t *>(ws);
-    a.arrive = reinterpret_cast<uint32_t *>(ws + p.wsCounters);
-    a.finalPre = reinterpret_cast<float *>(ws + p.wsFinal);
-    a.partial = reinterpret_cast<float *>(ws + p.wsFusedPartial);
+    a.status = reinterpret_cast<uint64_t *>(ws);
+    a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsFinal);
+    a.recs = reinterpret_cast<uint64_t *>(ws + p.wsFusedPartial);
     a.T = p.T;
     a.D = p.D;
     a.K = p.K;
@@ -546,31 +730,20 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, hipStream_t stream)
     a.normEps = p.normEps;
     a.hcEps = p.hcEps;
     a.invFlatDim = p.invFlatDim;
+    a.epoch = epoch;
     a.spinLimit = 1u << 20;  // about a second of polling per wait
 
-    const int64_t finalWords = p.fusedTiles * Rec<N>::FIN;
-    hipLaunchKernelGGL(fused_reset_kernel, dim3((unsigned)((finalWords + 255) / 256)), dim3(256), 0,
-                       stream, a.arrive, reinterpret_cast<uint32_t *>(a.finalPre),
-                       (int64_t)p.fusedTiles, finalWords, a.status);
-    err = hipGetLastError();
-    if (err != hipSuccess) {
-        return err;
-    }
     void *args[] = {&a};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<N, KS, kBf16>),
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16>),
                                       dim3((unsigned)p.fusedGrid), dim3(kFusedWaves * 64), args,
-                                      (unsigned)fused_lds_bytes<N, KS, kBf16>(), stream);
+                                      (unsigned)fused_lds_bytes<N, KP, kBf16>(), stream);
 }
 
 }  // namespace
 
-// Fused-path instantiations: n = 4 with KS in {8, 7, 4, 2, 1}.
+// Fused-path instantiations: n = 4 with KP in {4, 2, 1} (DW = 256, 128, 64).
 #define MHC_FUSED_DISPATCH(FN, ...)                                            \
-    switch (p.fusedDw / 32) {                                                  \
-    case 8:                                                                    \
-        return p.isBf16 ? FN<4, 8, true>(__VA_ARGS__) : FN<4, 8, false>(__VA_ARGS__); \
-    case 7:                                                                    \
-        return p.isBf16 ? FN<4, 7, true>(__VA_ARGS__) : FN<4, 7, false>(__VA_ARGS__); \
+    switch (p.fusedDw / 64) {                                                  \
     case 4:                                                                    \
         return p.isBf16 ? FN<4, 4, true>(__VA_ARGS__) : FN<4, 4, false>(__VA_ARGS__); \
     case 2:                                                                    \
@@ -581,12 +754,12 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, hipStream_t stream)
         break;                                                                 \
     }
 
-hipError_t launch_fused(const Plan &p, void *workspace, hipStream_t stream)
+hipError_t launch_fused(const Plan &p, void *workspace, uint32_t epoch, hipStream_t stream)
 {
     if (p.n != 4) {
         return hipErrorNotSupported;
     }
-    MHC_FUSED_DISPATCH(launch_fused_t, p, workspace, stream)
+    MHC_FUSED_DISPATCH(launch_fused_t, p, workspace, epoch, stream)
     return hipErrorNotSupported;
 }
 

@@ -13,12 +13,14 @@ enum class Path : int {
     kFused = 1,   // prep B, one persistent kernel: x read once, kept in registers
 };
 
-// Device status word values (first 4 bytes of the workspace).
+// Device status word (first 8 bytes of the workspace): the low half holds a
+// code, the high half the epoch of the launch that wrote it.  The fused path
+// writes (epoch, kDeviceTimeout) only when a wait runs out; the split path's
+// first kernel writes kDeviceOk into the low half.
 constexpr uint32_t kDeviceOk = 0u;
 constexpr uint32_t kDeviceTimeout = 0x7107u;
 
-// Bytes reserved at the head of the workspace for the status word and the
-// fused path's team counters header.
+// Bytes reserved at the head of the workspace for the status word.
 constexpr size_t kWsHeaderBytes = 256;
 
 struct Plan {
@@ -54,9 +56,8 @@ struct Plan {
     // workspace holds one launch at a time.
     size_t wsBsplit = 0;      // split: B fragments
     size_t wsPartial = 0;     // split: [S][T][M+1] partials
-    size_t wsFinal = 0;       // fused: per-tile hPre / invRms blocks
-    size_t wsFusedPartial = 0;// fused: per-(tile, slice) exchange records
-    size_t wsCounters = 0;    // fused: per-tile arrival counters
+    size_t wsFinal = 0;       // fused: per-tile hPre / invRms blocks (tagged words)
+    size_t wsFusedPartial = 0;// fused: per-(tile, slice) exchange records (tagged words)
     size_t wsTotal = 0;
 
     // Bound device pointers (caller memory).
@@ -73,21 +74,18 @@ struct Plan {
 
 // Kernel launchers (mhc_pre_kernels.hip).  Each returns the first HIP error.
 hipError_t launch_split(const Plan &plan, void *workspace, hipStream_t stream);
-hipError_t launch_fused(const Plan &plan, void *workspace, hipStream_t stream);
+// epoch: per-launch value mixed into the fused path's exchange tags; it must
+// differ from the epoch of every earlier launch that used this workspace.
+hipError_t launch_fused(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
 
 // Largest number of fused-path workgroups that can be co-resident on a device
 // with numCUs compute units, or -1 if the plan has no fused kernel.
 int fused_max_coresident(const Plan &plan, int numCUs);
 
-// Fused-path workspace geometry for n streams (floats): one exchange record
-// per (row tile, slice), one broadcast block per row tile, and one arrival
-// counter per row tile spaced 256 bytes apart.
-inline int fused_record_floats(int n)
-{
-    const int M = n * n + 2 * n;
-    return ((M + 1 + 1) / 2) * 2 * 16;
-}
-inline int fused_final_floats(int n) { return (((n + 1) * 16 + 31) / 32) * 32; }
-constexpr size_t kFusedCounterBytes = 256;
+// Fused-path workspace geometry for n streams, in 8-byte tagged words: one
+// exchange record of M + 1 columns x 16 rows per (row tile, slice), and one
+// broadcast block of n + 1 columns x 16 rows per row tile.
+inline int fused_record_words(int n) { return (n * n + 2 * n + 1) * 16; }
+inline int fused_bcast_words(int n) { return (n + 1) * 16; }
 
 }  // namespace mhc
