@@ -25,6 +25,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
+COPY_BYTES = 256 << 20  # size of the calibration copy (--copy-probe)
 
 WORKLOADS = {
     # name: (n, D, T, bf16, gamma, outlier rows x50)
@@ -102,6 +103,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=3, choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target duration of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a device copy of a known size (calibrates profiler byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); MhcPre shards "
@@ -142,6 +145,17 @@ def main() -> int:
     if status != 0:
         print(f"device status {status}", file=sys.stderr)
         return 1
+
+    if args.copy_probe:
+        # A plain device-to-device copy of exactly COPY_BYTES: under rocprofv3
+        # --pmc its FETCH_SIZE / WRITE_SIZE give the counters' scale factor.
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=device).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     b_alg = algorithmic_bytes(n, D, T, bf16, gamma_on)
     achieved = b_alg / (mean_ms * 1e-3) / 1e9

@@ -251,6 +251,9 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             p.path = mhc::Path::kSplit;
         }
     }
+    if (const char *launch = std::getenv("MHCPRE_LAUNCH")) {
+        p.fusedCooperative = std::strcmp(launch, "cooperative") == 0;
+    }
 
     // Workspace: header, then the split regions and the fused regions, which
     // overlap (one launch at a time per workspace).  Sizes depend on the

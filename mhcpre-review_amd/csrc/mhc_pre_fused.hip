@@ -40,9 +40,11 @@
 // when every word it read carries the expected tag; a block left over from an
 // earlier launch (another epoch) or filled with any constant never does.
 // Every wait is bounded by a spin limit; running out records kDeviceTimeout
-// with the launch's epoch in the status word instead of hanging.  The
-// cooperative launch keeps every workgroup resident, so a reducer is never
-// waiting on a workgroup that has not started.
+// with the launch's epoch in the status word instead of hanging.  The grid is
+// sized to the device's co-residency limit, so every workgroup is resident
+// when nothing else runs on the device (a cooperative launch, on request,
+// guarantees it even then); a reducer is then never waiting on a workgroup
+// that has not started.
 
 #include "mhc_pre_device.h"
 #include "mhc_pre_internal.h"
@@ -135,12 +137,6 @@ __device__ __forceinline__ uint32_t rec_tag(uint32_t pos, uint32_t epoch)
 __device__ __forceinline__ uint32_t bcast_tag(uint32_t pos, uint32_t epoch)
 {
     return (pos * 0x85EBCA77u) ^ epoch ^ 0xC2B2AE3Du;
-}
-
-__device__ __forceinline__ void st_word(uint64_t *p, float v, uint32_t tag)
-{
-    __hip_atomic_store(p, (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint64_t ld_word(const uint64_t *p)
@@ -251,7 +247,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     constexpr int KS = 2 * KP;  // 32-column MFMA k-steps per stream
     constexpr int DW = 64 * KP;
     constexpr int Q = CL::Q;
-    extern __shared__ u32x4_t bl[];  // [N*KS][NT][64] B fragments, then per-wave scratch
+    extern __shared__ u32x4_t bl[];  // [N*KS][NT][64] B fragments, per-wave scratch, staging
     static_assert(N == 4, "the fused path maps the n = 4 hPre columns to the 4 lane groups");
 
     const int P = a.P;
@@ -268,6 +264,9 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     const int64_t d0 = (int64_t)p * DW;
     const int64_t stride = (int64_t)numTeams * W;
     float *scratch = reinterpret_cast<float *>(bl + N * KS * NT * 64) + wave * RC::BWORDS;
+    uint64_t *stage = reinterpret_cast<uint64_t *>(reinterpret_cast<float *>(bl + N * KS * NT * 64) +
+                                                   W * RC::BWORDS) +
+                      wave * RC::WORDS;
     int64_t rt = (int64_t)team * W + wave;
 
     u32x4_t xr[N][KP][2];
@@ -498,30 +497,48 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
         const int di = rl & 3;
         const float ss = di == 0 ? gram[0] : di == 1 ? gram[1] : di == 2 ? gram[2] : gram[3];
 
-        // 2. Publish this slice's partials as tagged words (C fragment: lane
-        //    holds rows 4*grp + i of column slot 16t + rl).
+        // 2. Publish this slice's partials as tagged words.  The C fragment
+        //    (lane holds rows 4*grp + i of column slot 16t + rl) is written to
+        //    this wave's LDS staging record first, so that the device-scope
+        //    stores go out as whole 128-byte lines (8 lanes x 16 bytes per
+        //    column) instead of scattered 8-byte writes.
         {
             const uint32_t recBase = (uint32_t)((rt * Pi + p) * RC::WORDS);
-            uint64_t *rec = a.recs + (rt * Pi + p) * RC::WORDS;
+            auto put = [&](int w, float v) {
+                stage[w] = (uint64_t)__float_as_uint(v) | ((uint64_t)rec_tag(recBase + w, epoch) << 32);
+            };
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 4 * grp + i;
 #pragma unroll
                 for (int t = 0; t < Q; ++t) {
-                    const int w = RC::col(16 * t + rl) * 16 + r;
-                    st_word(rec + w, acc[t][i] + acc[Q + t][i], rec_tag(recBase + w, epoch));
+                    put(RC::col(16 * t + rl) * 16 + r, acc[t][i] + acc[Q + t][i]);
                 }
                 if constexpr (CL::kHalfTile) {
                     const float other = __shfl_xor(acc[2 * Q][i], 8);
                     if (rl < 8) {
-                        const int w = RC::col(16 * Q + rl) * 16 + r;
-                        st_word(rec + w, acc[2 * Q][i] + other, rec_tag(recBase + w, epoch));
+                        put(RC::col(16 * Q + rl) * 16 + r, acc[2 * Q][i] + other);
                     }
                 }
             }
             if (diagLane) {
-                const int w = N * 16 + rl;
-                st_word(rec + w, ss, rec_tag(recBase + w, epoch));
+                put(N * 16 + rl, ss);
+            }
+            // A wave's LDS accesses complete in order; the barrier keeps the
+            // compiler from moving the reads below above the writes.
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            const __amdgpu_buffer_rsrc_t rr =
+                make_rsrc(a.recs + (rt * Pi + p) * RC::WORDS, RC::WORDS * 8);
+            constexpr int CHUNKS = RC::WORDS / 2;  // 16-byte chunks of the record
+#pragma unroll
+            for (int k = 0; k < (CHUNKS + 63) / 64; ++k) {
+                const int j = laneO + 64 * k;
+                if (j < CHUNKS) {
+                    const u32x4_t v = *reinterpret_cast<const u32x4_t *>(stage + 2 * j);
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), rr,
+                        16 * j, 0, kCpolDev);
+                }
             }
         }
         // The previous tile's hPost / hRes fill the time the other slices
@@ -564,6 +581,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
             ir1 = __shfl(ir1, 8 * N + it % 8);
             if (laneO < NIT) {
                 const float bc = c < N ? a.bias[c] : 0.f;
+                u32x4_t wv;
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     const float ir = e == 0 ? ir0 : ir1;
@@ -571,12 +589,18 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
                     const float v = c < N ? ref_sigmoid(mix * (ir * alphaPre), bc, a.hcEps) : ir;
                     const int idx = c * 16 + r0 + e;
                     scratch[idx] = v;
-                    st_word(blk + idx, v, bcast_tag(blkBase + idx, epoch));
+                    wv[2 * e] = __float_as_uint(v);
+                    wv[2 * e + 1] = bcast_tag(blkBase + idx, epoch);
                     const int64_t row = rt * 16 + r0 + e;
                     if (c < N && a.hPre != nullptr && row < a.T) {
                         a.hPre[row * N + c] = v;
                     }
                 }
+                // Two tagged words (rows r0, r0 + 1) per lane: 8 lanes fill
+                // a column's 128-byte line.
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, wv),
+                    make_rsrc(blk, RC::BWORDS * 8), (c * 16 + r0) * 8, 0, kCpolDev);
             }
             preC = scratch[grp * 16 + rl];
             invRms = scratch[N * 16 + rl];
@@ -669,7 +693,8 @@ template <int N, int KP, bool kBf16>
 size_t fused_lds_bytes()
 {
     return (size_t)N * 2 * KP * Shape<N>::NT * 64 * sizeof(u32x4_t) +
-           (size_t)kFusedWaves * Rec<N>::BWORDS * sizeof(float);
+           (size_t)kFusedWaves * Rec<N>::BWORDS * sizeof(float) +
+           (size_t)kFusedWaves * Rec<N>::WORDS * sizeof(uint64_t);
 }
 
 template <int N, int KP, bool kBf16>
@@ -733,10 +758,16 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
     a.epoch = epoch;
     a.spinLimit = 1u << 20;  // about a second of polling per wait
 
+    const unsigned lds = (unsigned)fused_lds_bytes<N, KP, kBf16>();
+    if (!p.fusedCooperative) {
+        hipLaunchKernelGGL((fused_kernel<N, KP, kBf16>), dim3((unsigned)p.fusedGrid),
+                           dim3(kFusedWaves * 64), lds, stream, a);
+        return hipGetLastError();
+    }
     void *args[] = {&a};
     return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16>),
                                       dim3((unsigned)p.fusedGrid), dim3(kFusedWaves * 64), args,
-                                      (unsigned)fused_lds_bytes<N, KP, kBf16>(), stream);
+                                      lds, stream);
 }
 
 }  // namespace

@@ -36,6 +36,14 @@ struct Plan {
     bool isBf16 = true;
     bool hasGamma = false;
     bool hasHPre = false;
+    // Fused path launch.  By default a plain launch of a grid sized to the
+    // device's co-residency limit: every workgroup is resident as long as no
+    // other kernel occupies the device, and the kernel's bounded waits turn
+    // any other case into a reported timeout rather than a hang.
+    // MHCPRE_LAUNCH=cooperative selects a cooperative launch, which
+    // guarantees co-residency next to concurrent work at the cost of a
+    // slower dispatch (about 20 us per launch on MI355X).
+    bool fusedCooperative = false;
     float normEps = 1e-6f;
     float hcEps = 1e-6f;
     float invFlatDim = 0.f;  // fl(1.0f / K), as code/op_host/mhc_pre.cpp:154

@@ -35,7 +35,7 @@ def to_device(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, lead=None):
 
 
 def run_gpu(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, norm_eps=1e-6, hc_eps=1e-6,
-            lead=None, h_pre=True, force_path=None):
+            lead=None, h_pre=True, force_path=None, launch=None):
     import os
 
     import torch
@@ -43,10 +43,13 @@ def run_gpu(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, norm_eps=1e-6
     xt, pt, at, bt, gt = to_device(pkg, device, x_bits, is_bf16, phi, alpha, bias, gamma, lead)
     if force_path is not None:
         os.environ["MHCPRE_FORCE_PATH"] = force_path
+    if launch is not None:
+        os.environ["MHCPRE_LAUNCH"] = launch
     try:
         op = pkg.MhcPreOp(xt, pt, at, bt, gt, norm_eps, hc_eps, h_pre=True if h_pre else None)
     finally:
         os.environ.pop("MHCPRE_FORCE_PATH", None)
+        os.environ.pop("MHCPRE_LAUNCH", None)
     _say(f"  path={op.path}")
     op.launch()
     torch.cuda.synchronize()
@@ -89,6 +92,21 @@ def test_config_full_parity(pkg, orc, device, cfg, force):
     out = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, force_path=force)
     ref = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
     check(out, ref, x, case.is_bf16, orc)
+
+
+def test_cooperative_launch_matches(pkg, orc, device):
+    """The cooperative launch mode (MHCPRE_LAUNCH=cooperative) runs the same
+    fused kernel: bit-identical outputs to the default launch, and parity."""
+    case = CONFIGS[2]
+    _say(f"[parity] config 2 cooperative launch: {case}")
+    x, phi, alpha, bias, gamma = make_case(case)
+    coop = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, launch="cooperative")
+    plain = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma)
+    assert coop["path"] == plain["path"] == "fused"
+    for k in ("h_in", "h_post", "h_res", "h_pre"):
+        assert np.array_equal(coop[k], plain[k]), k
+    ref = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
+    check(coop, ref, x, case.is_bf16, orc)
 
 
 @pytest.mark.parametrize("B,S,n,D,has_gamma,is_bf16", E3_CASES)
