@@ -5,13 +5,16 @@ Workload (default): the headline prefill shape n=4, D=7168, T=8192, bf16 x,
 gamma on -- one "step" is one MhcPre launch over all T rows with every input
 already resident in HBM.  Prints ONE JSON line.
 
-  value      tokens/s = T / (mean launch time over the timed steps)
+  value      tokens/s = T / (mean launch time over the timed steps), each launch
+             bracketed by HIP events on the stream it is launched on
   roofline   algorithmic bytes per launch / mean launch time, against 8 TB/s;
              bytes = x + phi + gamma + bias + alpha + hIn + hPost + hRes, each
-             counted once (hPre is not part of the operator contract)
+             counted once (hPre is not part of the operator contract);
+             traffic = HBM bytes per launch from the committed rocprofv3 PMC
+             record for the workload (profiles/*.traffic.json), when present
   cpu_baseline  the scalar C oracle (reference floating-point order), OpenMP
-             over rows, timed on this host on a bounded row sample of the
-             same inputs
+             over rows, timed on this host on a bounded sample of the same
+             inputs (about --cpu-seconds of work)
 """
 from __future__ import annotations
 
@@ -68,7 +71,11 @@ def make_inputs(cfg: int, device):
 
 
 def cpu_baseline(x, phi, alpha, bias, gamma, bf16: bool, target_s: float) -> dict:
-    """Time the C oracle on a row sample of the same inputs (all host cores)."""
+    """Time the C oracle (reference fp order, OpenMP over rows) on this host.
+
+    The sample is the full workload's rows, processed in blocks of up to 512
+    rows and repeated until about target_s seconds of CPU time have passed
+    (a bounded sample; the rate is rows / second)."""
     import numpy as np
     import torch
 
@@ -79,20 +86,34 @@ def cpu_baseline(x, phi, alpha, bias, gamma, bf16: bool, target_s: float) -> dic
     phi_h = phi.cpu().numpy()
     alpha_h, bias_h = alpha.cpu().numpy(), bias.cpu().numpy()
     g_h = gamma.cpu().numpy() if gamma is not None else None
-
-    def run(rows: int) -> float:
-        xs = x[:rows].view(torch.int16).cpu().numpy().view(np.uint16)
-        t0 = time.perf_counter()
+    x_h = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    block = min(T, 512)
+    rows = 0
+    t0 = time.perf_counter()
+    elapsed = 0.0
+    start = 0
+    while elapsed < target_s:
+        xs = x_h[start:start + block]
         orc.mhc_pre(xs, bf16, phi_h, alpha_h, bias_h, g_h, nthreads=threads)
-        return time.perf_counter() - t0
+        rows += xs.shape[0]
+        start = (start + block) % T
+        elapsed = time.perf_counter() - t0
+    return {"value": rows / elapsed, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} rows ({rows / T:.2f} passes over the {T} rows of the same inputs, "
+                      f"in blocks of {block}) in {elapsed:.1f} s, OpenMP over rows "
+                      f"({threads} threads)"}
 
-    probe = max(threads, 8)
-    dt = run(probe)
-    rows = int(min(T, max(probe, probe * target_s / max(dt, 1e-6))))
-    dt = run(rows)
-    return {"value": rows / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"first {rows} of {T} rows of the same inputs, {dt:.2f} s, "
-                      f"OpenMP over rows ({threads} threads)"}
+
+def measured_traffic(workload: str, path: str):
+    """HBM bytes per launch for this workload from the committed rocprofv3 PMC
+    record (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size), or None."""
+    if path != "fused":
+        return None
+    for f in sorted((ROOT / "profiles").glob("*.traffic.json")):
+        rec = json.loads(f.read_text())
+        if rec.get("workload") == workload:
+            return rec
+    return None
 
 
 def main() -> int:
@@ -159,6 +180,9 @@ def main() -> int:
 
     b_alg = algorithmic_bytes(n, D, T, bf16, gamma_on)
     achieved = b_alg / (mean_ms * 1e-3) / 1e9
+    workload = (f"mhc_pre n={n} D={D} T={T} {'bf16' if bf16 else 'fp16'} "
+                f"gamma={'on' if gamma_on else 'off'}")
+    traffic = measured_traffic(workload, op.path)
     result = {
         "metric": METRIC,
         "value": T / (mean_ms * 1e-3),
@@ -172,13 +196,14 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16" if bf16 else "fp16",
         "data": "synthetic",
-        "config": {"workload": f"mhc_pre n={n} D={D} T={T} {'bf16' if bf16 else 'fp16'} "
-                               f"gamma={'on' if gamma_on else 'off'}",
+        "config": {"workload": workload,
                    "n": n, "D": D, "T": T, "gamma": gamma_on, "path": op.path,
                    "median_us": durs[len(durs) // 2] * 1e3, "min_us": durs[0] * 1e3,
-                   "algorithmic_bytes": b_alg},
+                   "algorithmic_bytes": b_alg,
+                   "traffic_source": traffic["summary"] if traffic else None},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic["traffic_bytes"] if traffic else None},
     }
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(x, phi, alpha, bias, gamma, bf16,
