@@ -17,8 +17,10 @@
  * cloud_runner/runner.cpp:443-445,459): phase 1 validates the tensors, sizes
  * the device workspace and returns an executor bound to the tensors' device
  * addresses; phase 2 launches on a HIP stream.  The caller owns every device
- * buffer, including the workspace.  The executor is immutable after creation:
- * it may be launched any number of times (the reference probe relaunches one
+ * buffer, including the workspace, whose contents need not be preserved
+ * between launches.  An executor's plan is immutable after creation (it only
+ * records the epoch of its latest launch, for mhcPreQueryDeviceStatus): it may
+ * be launched any number of times (the reference probe relaunches one
  * executor, cloud_runner/probe_e1e2.cpp:312-326) and from several host threads
  * on different streams, provided the launches do not share a workspace
  * concurrently.  No function aborts; every failure is a status code.
@@ -116,6 +118,15 @@ MHC_API int mhcPreGetWorkspaceSizeWithHPre(const mhcTensor *x, const mhcTensor *
  * Phase 2.  Replaces aclnnMhcPre (cloud_runner/runner.cpp:459,472): enqueues
  * the operator on `stream` (NULL = the null stream) and returns without
  * waiting.  The workspace must hold at least the bytes phase 1 returned.
+ *
+ * The fused kernel's workgroups wait on each other (bounded), so its grid is
+ * sized to what the device holds at once.  By default it is a plain launch:
+ * every workgroup is resident unless another kernel occupies the device at
+ * the same time, in which case a wait can expire and
+ * mhcPreQueryDeviceStatus reports MHC_STATUS_DEVICE_TIMEOUT (no hang).  With
+ * the environment variable MHCPRE_LAUNCH=cooperative at phase 1 the executor
+ * uses a cooperative launch, which guarantees co-residency next to concurrent
+ * work but dispatches more slowly (about 20 us per launch on MI355X).
  */
 MHC_API int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor,
            hipStream_t stream);
@@ -124,10 +135,11 @@ MHC_API int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *exec
 MHC_API int mhcPreExecutorDestroy(mhcPreExecutor *executor);
 
 /*
- * Device-side status of the last completed launch that used `workspace`:
- * MHC_STATUS_SUCCESS, or MHC_STATUS_DEVICE_TIMEOUT if a bounded wait between
- * workgroups expired.  Synchronizes `stream` first.  No reference counterpart
- * (the reference detects a hang only by the caller's own wait,
+ * Device-side status of this executor's latest launch on `workspace`:
+ * MHC_STATUS_SUCCESS, or MHC_STATUS_DEVICE_TIMEOUT if one of its bounded
+ * waits between workgroups expired (the outputs of such a launch are not
+ * valid).  Synchronizes `stream` first.  No reference counterpart (the
+ * reference detects a hang only by the caller's own wait,
  * cloud_runner/probe_e1e2.cpp:295).
  */
 MHC_API int mhcPreQueryDeviceStatus(void *workspace, uint64_t workspaceSize,
