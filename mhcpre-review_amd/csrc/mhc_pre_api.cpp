@@ -59,26 +59,39 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Compute-unit count of the current device, cached per device.
-int device_cu_count(int &device)
+// Compute units and XCDs of the current device, cached per device.
+struct DeviceShape {
+    int cus = 0;
+    int xcds = 0;
+};
+
+bool device_shape(int &device, DeviceShape &out)
 {
     constexpr int kMaxDevices = 64;
     static std::mutex mu;
-    static int cache[kMaxDevices] = {};
+    static DeviceShape cache[kMaxDevices] = {};
     if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
-        return -1;
+        return false;
     }
     std::lock_guard<std::mutex> lock(mu);
-    if (cache[device] == 0) {
+    if (cache[device].cus == 0) {
         int cus = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) !=
                 hipSuccess ||
             cus <= 0) {
-            return -1;
+            return false;
         }
-        cache[device] = cus;
+        int xcds = 0;
+        if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device) != hipSuccess ||
+            xcds <= 0 || cus % xcds != 0) {
+            (void)hipGetLastError();
+            xcds = 1;
+        }
+        cache[device].cus = cus;
+        cache[device].xcds = xcds;
     }
-    return cache[device];
+    out = cache[device];
+    return true;
 }
 
 // Launch epochs: process-wide, strictly increasing from a start that differs
@@ -245,10 +258,17 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             }
         }
     }
-    p.path = p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit;
+    // Strip path (n = 4): slices of 256 columns.
+    if (n == 4 && (D % 256) == 0) {
+        p.stripP = static_cast<int>(D / 256);
+    }
+    p.path = p.stripP > 0 ? mhc::Path::kStrip
+                          : (p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit);
     if (const char *force = std::getenv("MHCPRE_FORCE_PATH")) {
         if (std::strcmp(force, "split") == 0) {
             p.path = mhc::Path::kSplit;
+        } else if (std::strcmp(force, "fused") == 0 && p.fusedP > 0) {
+            p.path = mhc::Path::kFused;
         }
     }
     if (const char *launch = std::getenv("MHCPRE_LAUNCH")) {
@@ -347,15 +367,32 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
     }
     hipError_t err = hipSuccess;
     bool done = false;
-    if (p.path == mhc::Path::kFused) {
-        // Teams of fusedP workgroups must be co-resident (cooperative launch);
-        // a device too small for one team runs the split path instead.
-        int device = -1;
-        const int cus = device_cu_count(device);
-        if (cus < 0) {
-            return MHC_STATUS_HIP_ERROR;
+    int device = -1;
+    DeviceShape shape;
+    if (p.path != mhc::Path::kSplit && !device_shape(device, shape)) {
+        return MHC_STATUS_HIP_ERROR;
+    }
+    if (p.path == mhc::Path::kStrip) {
+        // One workgroup per CU, all co-resident; each XCD's CUs hold at least
+        // one team of stripP slice workgroups and one reducer workgroup.
+        const int perXcd = shape.cus / shape.xcds;
+        const int teamsPerXcd = perXcd / (p.stripP + 1);
+        if (teamsPerXcd >= 1 && mhc::strip_max_coresident(p, shape.cus) >= shape.cus) {
+            mhc::Plan lp = p;
+            lp.stripXcds = shape.xcds;
+            lp.stripTeamsPerXcd = teamsPerXcd;
+            lp.stripR = perXcd / teamsPerXcd - p.stripP;
+            lp.stripGrid = shape.cus;
+            const uint32_t epoch = next_epoch();
+            executor->lastEpoch.store(epoch, std::memory_order_relaxed);
+            err = mhc::launch_strip(lp, workspace, epoch, stream);
+            done = true;
         }
-        const int coresident = mhc::fused_max_coresident(p, cus);
+    }
+    if (!done && p.fusedP > 0 && p.path != mhc::Path::kSplit) {
+        // Teams of fusedP workgroups must be co-resident; a device too small
+        // for one team runs the split path instead.
+        const int coresident = mhc::fused_max_coresident(p, shape.cus);
         if (coresident >= p.fusedP) {
             mhc::Plan lp = p;
             lp.fusedTeams = coresident / p.fusedP;
@@ -438,7 +475,17 @@ int mhcPreExecutorPath(const mhcPreExecutor *executor, const char **name)
     if (executor == nullptr || name == nullptr) {
         return MHC_STATUS_NULL_ARGUMENT;
     }
-    *name = executor->plan.path == mhc::Path::kFused ? "fused" : "split";
+    switch (executor->plan.path) {
+    case mhc::Path::kStrip:
+        *name = "strip";
+        break;
+    case mhc::Path::kFused:
+        *name = "fused";
+        break;
+    default:
+        *name = "split";
+        break;
+    }
     return MHC_STATUS_SUCCESS;
 }
 

@@ -10,7 +10,8 @@ namespace mhc {
 // Kernel paths an executor can launch.
 enum class Path : int {
     kSplit = 0,   // prep B, split-K MFMA GEMM + sumsq partials, epilogue + hIn (x read twice)
-    kFused = 1,   // prep B, one persistent kernel: x read once, kept in registers
+    kFused = 1,   // one persistent kernel: x read once, kept in registers
+    kStrip = 2,   // one persistent kernel: XCD-local teams, B in registers, x in a register ring
 };
 
 // Device status word (first 8 bytes of the workspace): the low half holds a
@@ -60,6 +61,16 @@ struct Plan {
     int fusedTeams = 0;       // teams of fusedP workgroups
     int64_t fusedTiles = 0;   // 16-row tiles
 
+    // Strip path (n = 4, D % 256 == 0): P slice workgroups of 256 columns and
+    // R reducer workgroups per team, teams formed inside one XCD.  stripR,
+    // stripXcds, stripTeamsPerXcd and stripGrid are filled per launch from
+    // the device.
+    int stripP = 0;
+    int stripR = 0;
+    int stripXcds = 0;
+    int stripTeamsPerXcd = 0;
+    int stripGrid = 0;
+
     // Workspace layout (byte offsets).  The two paths' regions overlap: a
     // workspace holds one launch at a time.
     size_t wsBsplit = 0;      // split: B fragments
@@ -85,6 +96,12 @@ hipError_t launch_split(const Plan &plan, void *workspace, hipStream_t stream);
 // epoch: per-launch value mixed into the fused path's exchange tags; it must
 // differ from the epoch of every earlier launch that used this workspace.
 hipError_t launch_fused(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
+
+hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
+
+// Workgroups of the strip kernel that can be resident per CU (x numCUs), or
+// -1 if the plan has no strip kernel.
+int strip_max_coresident(const Plan &plan, int numCUs);
 
 // Largest number of fused-path workgroups that can be co-resident on a device
 // with numCUs compute units, or -1 if the plan has no fused kernel.

@@ -1,0 +1,815 @@
+// Strip kernel for gfx950 (n = 4, D % 256 == 0): x is read from HBM once,
+// held in VGPRs in a ring of row tiles, and the cross-workgroup exchange of
+// the K-reduction runs in the shadow of the x stream.
+//
+// Teams.  The workgroups of one XCD form teams: P = D / 256 slice workgroups
+// and R reducer workgroups each.  Workgroup g runs on XCD g mod X (the
+// hardware dispatches workgroups round-robin over the X XCDs), so a team's
+// exchange stays inside one XCD's L2.  The exchange itself uses device-scope
+// accesses, so results do not depend on where a workgroup actually runs;
+// only the speed does.  Team t owns row tiles t, t + numTeams, t + 2 numTeams,
+// ... (16 rows each); its k-th tile is its "step k".
+//
+// Slice workgroup p (4 waves, one per SIMD).  Wave w owns the 64-column strip
+// [256p + 64w, 256p + 64w + 64) of every stream: 256 values of K, whose B
+// operand (gamma * phi split into bf16 hi + lo, 3 column tiles x 8 k-steps)
+// it keeps in 96 VGPRs for the whole launch.  x of a tile is 16 rows x 4
+// streams x 64 columns = 8 KB per wave (32 VGPRs), loaded as whole 128-byte
+// lines (register (s, h) holds, in lane l, row 8h + (l & 7) and the 8 columns
+// at 8(l >> 4) + 32((l >> 3) & 1) of stream s) and held in a ring of L tiles.
+// Step k of a wave:
+//   1. MFMA of tile k against the B registers (a DPP row_ror:8 turns a pair
+//      of line registers into the A fragments of two k-steps) and a Gram
+//      MFMA of the same fragments, whose diagonal is the sum of squares;
+//   2. the four waves' partials (M mix columns + sumsq, 16 rows) meet in LDS
+//      and are summed in wave order into the slice's record, which is stored
+//      as tagged words (below) in whole 128-byte lines;
+//   3. hIn of tile k - E from the registers, with hPre from the tile's
+//      broadcast block, polled DP steps earlier;
+//   4. a poll of the broadcast block of tile k - E + DP, then the loads of
+//      tile k - E + L into the registers hIn just freed.
+// So the loads of L - E tiles are in flight ahead of the MFMA while E tiles
+// wait for their hPre.
+//
+// Reducer workgroup (4 waves).  Reducer wave i of a team takes the team's
+// steps k = i, i + 4R, ...: it polls the P records of the tile, sums the hPre
+// mix columns and the sum of squares over the slices in slice order,
+// evaluates invRms and hPre, publishes hPre as a broadcast block of tagged
+// words, then sums the hPost / hRes columns and writes those outputs.
+//
+// Exchange words.  Every exchanged value is one 8-byte word: the fp32 bits in
+// the low half and a tag in the high half, written and read as single-copy
+// atomic accesses at device scope (sc1).  The tag is a hash of the word's
+// position XOR a per-launch epoch, so a word holds the current value exactly
+// when its tag matches: no arrival counter, no release wait, no reset of the
+// workspace between launches.  Every wait is bounded by a spin limit; running
+// out records kDeviceTimeout with the launch's epoch in the status word
+// instead of hanging.  The grid is one workgroup per CU, all co-resident when
+// nothing else occupies the device.
+
+#include "mhc_pre_device.h"
+#include "mhc_pre_internal.h"
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+
+namespace mhc {
+namespace {
+
+using namespace dev;
+
+constexpr int kWaves = 4;                   // waves per workgroup, one per SIMD
+constexpr int kStripCols = 64;              // x columns of each stream per wave
+constexpr int kSlice = kWaves * kStripCols; // columns per slice
+constexpr int kRing = 8;                    // L: x tiles held per wave
+constexpr int kLag = 5;                     // E: hIn of tile k runs at step k + E
+constexpr int kPollAhead = 2;               // DP: broadcast poll issued DP steps before use
+static_assert(kLag < kRing && kPollAhead <= kLag, "ring geometry");
+
+struct StripArgs {
+    const uint16_t *x;
+    const float *phi;
+    const float *gamma;
+    const float *alpha;
+    const float *bias;
+    uint16_t *hIn;
+    float *hPost;
+    float *hRes;
+    float *hPre;
+    uint64_t *recs;    // [RT][P] records of Rec<N>::WORDS tagged words
+    uint64_t *bcast;   // [RT] blocks of Rec<N>::BWORDS tagged words
+    uint64_t *status;  // (epoch << 32) | kDeviceTimeout after a timeout
+    int64_t T;
+    int64_t D;
+    int64_t K;
+    int64_t RT;
+    int P;            // slice workgroups per team (D / 256)
+    int R;            // reducer workgroups per team
+    int nXcd;         // XCDs of the device
+    int teamsPerXcd;  // teams formed from the workgroups of one XCD
+    int numTeams;     // nXcd * teamsPerXcd
+    float normEps;
+    float hcEps;
+    float invFlatDim;
+    uint32_t epoch;
+    uint32_t spinLimit;
+};
+
+// Column slots of the [hi | lo] B operand, NT = 2M/16 tiles of 16 lanes:
+// tiles [0,Q) hold hi of j = 16t + l, tiles [Q,2Q) lo of the same j, so hi and
+// lo of a column meet in the same lane; when M % 16 == 8 the last tile holds
+// hi (lanes 0-7) and lo (lanes 8-15) of j = 16Q + (l & 7).
+template <int M>
+struct ColLayout {
+    static constexpr int Q = M / 16;
+    static constexpr bool kHalfTile = (M % 16) == 8;
+    static_assert(M % 16 == 0 || M % 16 == 8, "M = n*n + 2n is 24, 48 or 80");
+    __device__ static void slot(int c, bool &lo, int &j)
+    {
+        const int t = c >> 4, l = c & 15;
+        if (t < Q) {
+            lo = false;
+            j = 16 * t + l;
+        } else if (t < 2 * Q) {
+            lo = true;
+            j = 16 * (t - Q) + l;
+        } else {
+            lo = l >= 8;
+            j = 16 * Q + (l & 7);
+        }
+    }
+    static constexpr bool has_hi(int t) { return t < Q || t == 2 * Q; }
+};
+
+// Record of one (row tile, slice), column-major: column c holds its 16 rows
+// as 16 consecutive tagged words (128 bytes).  Column N is the sum of
+// squares; mix column j sits at column j (j < N, the hPre columns) or j + 1.
+// The per-tile broadcast block holds hPre columns 0..N-1, 16 rows each.
+template <int N>
+struct Rec {
+    static constexpr int M = N * N + 2 * N;
+    static constexpr int COLS = M + 1;
+    static constexpr int WORDS = COLS * 16;
+    static constexpr int CHUNKS = WORDS / 2;  // 16-byte chunks
+    static constexpr int BWORDS = N * 16;
+    __device__ static int col(int j) { return j < N ? j : j + 1; }
+};
+
+__device__ __forceinline__ uint32_t rec_tag(uint32_t pos, uint32_t epoch)
+{
+    return (pos * 0x9E3779B1u) ^ epoch;
+}
+__device__ __forceinline__ uint32_t bcast_tag(uint32_t pos, uint32_t epoch)
+{
+    return (pos * 0x85EBCA77u) ^ epoch ^ 0xC2B2AE3Du;
+}
+
+__device__ __forceinline__ uint64_t ld_word(const uint64_t *p)
+{
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kCpolNt = 2;    // nontemporal: x and hIn are streamed once
+constexpr int kCpolDev = 16;  // sc1: device-scope coherent
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, 0x00020000);
+}
+
+template <int kCpol>
+__device__ __forceinline__ void store16(const u32x4_t &v, __amdgpu_buffer_rsrc_t r, int off)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, off, 0, kCpol);
+}
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load of the wave, which would drain the x ring.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ void record_timeout(const StripArgs &a, int lane)
+{
+    if (lane == 0) {
+        __hip_atomic_store(a.status, ((uint64_t)a.epoch << 32) | kDeviceTimeout, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Sums over the P slice records of a tile, for record columns c0 .. c0+NC-1
+// and all 16 rows, checking every word's tag.  Lane l takes item
+// it = l % (8 NC) (column c0 + it/8, rows 2(it%8) and 2(it%8) + 1, one 16-byte
+// load per slice) and slice group sg = l / (8 NC), and adds slices sg,
+// sg + NSG, ... in increasing order; the groups are then added in order
+// 0, 1, ..., NSG-1, so the result is a fixed-order sum.  Loads are issued U
+// slices per lane at a time.  Lanes it < 8 NC return the two row totals of
+// their item; valid is true when every word read carried the expected tag.
+template <int NC, int COLS, int U>
+__device__ __forceinline__ float2 sum_records(__amdgpu_buffer_rsrc_t r, int c0, int P, int lane,
+                                              uint32_t tileBase, uint32_t epoch, bool &valid)
+{
+    constexpr int NIT = 8 * NC;
+    constexpr int NSG = 64 / NIT;
+    static_assert(NSG >= 1, "at most 8 columns per call");
+    const int it = lane % NIT;
+    const int sg = lane / NIT;
+    const bool act = sg < NSG;
+    const int c = c0 + it / 8;
+    const int row0 = 2 * (it % 8);
+    float2 acc = make_float2(0.f, 0.f);
+    bool ok = true;
+    for (int q0 = 0; q0 < P; q0 += NSG * U) {
+        u32x4_t t[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = q0 + sg + NSG * u;
+            t[u] = (act && q < P)
+                       ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         r, ((q * COLS + c) * 16 + row0) * 8, 0,
+                                                         kCpolDev))
+                       : u32x4_t{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = q0 + sg + NSG * u;
+            if (act && q < P) {
+                const uint32_t pos = tileBase + (uint32_t)((q * COLS + c) * 16 + row0);
+                ok = ok && t[u][1] == rec_tag(pos, epoch) && t[u][3] == rec_tag(pos + 1u, epoch);
+                acc.x = acc.x + __uint_as_float(t[u][0]);
+                acc.y = acc.y + __uint_as_float(t[u][2]);
+            }
+        }
+    }
+    float2 tot = acc;
+#pragma unroll
+    for (int k = 1; k < NSG; ++k) {
+        tot.x = tot.x + __shfl(acc.x, it + k * NIT);
+        tot.y = tot.y + __shfl(acc.y, it + k * NIT);
+    }
+    valid = __all(ok);
+    return tot;
+}
+
+// sum_records, repeated until every word carries its tag (or the spin limit
+// runs out, which is recorded in the status word).
+// After a wave's first timeout (timedOut set) it no longer waits at all, so
+// a launch whose exchange failed ends after one spin limit per wave.
+template <int NC, int COLS, int U>
+__device__ __forceinline__ float2 poll_records(const StripArgs &a, __amdgpu_buffer_rsrc_t r, int c0,
+                                               int lane, uint32_t tileBase, bool &timedOut)
+{
+    float2 tot;
+    bool valid = false;
+    for (uint32_t spins = 0;; ++spins) {
+        tot = sum_records<NC, COLS, U>(r, c0, a.P, lane, tileBase, a.epoch, valid);
+        if (valid || timedOut) {
+            break;
+        }
+        if (spins >= a.spinLimit) {
+            record_timeout(a, lane);
+            timedOut = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return tot;
+}
+
+// A fragments of k-steps 2q and 2q + 1 from the line-layout registers r0
+// (rows 0-7) and r1 (rows 8-15): lanes with bit 3 set take the other
+// register's lane l ^ 8 (DPP row_ror:8 with banks 2-3 or 0-1 enabled).
+__device__ __forceinline__ void lines_to_frags(const u32x4_t &r0, const u32x4_t &r1, u32x4_t &k0,
+                                               u32x4_t &k1)
+{
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        k0[w] = (uint32_t)__builtin_amdgcn_update_dpp((int)r0[w], (int)r1[w], 0x128, 0xF, 0xC, false);
+        k1[w] = (uint32_t)__builtin_amdgcn_update_dpp((int)r1[w], (int)r0[w], 0x128, 0xF, 0x3, false);
+    }
+}
+
+__device__ __forceinline__ f32x4_t mfma16_f16(const u32x4_t &a, const u32x4_t &b, const f32x4_t &c)
+{
+    typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// Reducer wave: the team's steps k = rw, rw + nrw, ...
+template <int N>
+__device__ __forceinline__ void reducer_role(const StripArgs &a, int team, int64_t ntiles, int rw,
+                                             int nrw, int lane)
+{
+    using RC = Rec<N>;
+    constexpr int M = RC::M;
+    constexpr int COLS = RC::COLS;
+    const float alphaPre = a.alpha[0];
+    const float alphaPost = a.alpha[1];
+    const float alphaRes = a.alpha[2];
+    const uint32_t epoch = a.epoch;
+    const int P = a.P;
+    bool timedOut = false;
+    for (int64_t k = rw; k < ntiles; k += nrw) {
+        const int64_t rt = (int64_t)team + (int64_t)a.numTeams * k;
+        const __amdgpu_buffer_rsrc_t tr = make_rsrc(a.recs + rt * P * RC::WORDS, P * RC::WORDS * 8);
+        const uint32_t tileBase = (uint32_t)(rt * P * RC::WORDS);
+
+        // Cheap readiness poll first: the last hPre chunk (sum of squares,
+        // rows 14-15) of every slice record, one 16-byte load per lane.
+        {
+            const int cc = N * 16 + 14;
+            for (uint32_t spins = 0;; ++spins) {
+                bool ok = true;
+                if (lane < P) {
+                    const u32x4_t t = __builtin_bit_cast(
+                        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                     tr, (lane * COLS * 16 + cc) * 8, 0, kCpolDev));
+                    const uint32_t pos = tileBase + (uint32_t)(lane * COLS * 16 + cc);
+                    ok = t[1] == rec_tag(pos, epoch) && t[3] == rec_tag(pos + 1u, epoch);
+                }
+                if (__all(ok) || timedOut) {
+                    break;
+                }
+                if (spins >= a.spinLimit) {
+                    record_timeout(a, lane);
+                    timedOut = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        }
+
+        // hPre mix columns 0..N-1 and the sum of squares (column N).
+        constexpr int NIT = 8 * (N + 1);
+        const float2 tot = poll_records<N + 1, COLS, 32>(a, tr, 0, lane, tileBase, timedOut);
+        const int it = lane % NIT;
+        const int c = it / 8;
+        const int r0 = 2 * (it % 8);
+        // invRms of rows 2(l % 8), 2(l % 8) + 1 in every lane, from the
+        // sum-of-squares lanes 8N + l % 8.
+        const float irA = ref_inv_rms(tot.x, a.invFlatDim, a.normEps);
+        const float irB = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
+        const float ir0 = __shfl(irA, 8 * N + (lane & 7));
+        const float ir1 = __shfl(irB, 8 * N + (lane & 7));
+        if (lane < 8 * N) {
+            const float bc = a.bias[c];
+            u32x4_t wv;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float ir = e == 0 ? ir0 : ir1;
+                const float mix = e == 0 ? tot.x : tot.y;
+                const float v = ref_sigmoid(mix * (ir * alphaPre), bc, a.hcEps);
+                const int idx = c * 16 + r0 + e;
+                wv[2 * e] = __float_as_uint(v);
+                wv[2 * e + 1] = bcast_tag((uint32_t)(rt * RC::BWORDS) + idx, epoch);
+                const int64_t row = rt * 16 + r0 + e;
+                if (a.hPre != nullptr && row < a.T) {
+                    a.hPre[row * N + c] = v;
+                }
+            }
+            store16<kCpolDev>(wv, make_rsrc(a.bcast + rt * RC::BWORDS, RC::BWORDS * 8),
+                              (c * 16 + r0) * 8);
+        }
+
+        // hPost / hRes: record columns N+1 .. M (mix columns N .. M-1), up to
+        // 8 columns per pass.
+        auto post_res = [&](const float2 &v2, int cc0, int ncols) {
+            const int itp = lane % (8 * ncols);
+            const int cp = cc0 + itp / 8;
+            const int rp = 2 * (itp % 8);
+            if (lane < 8 * ncols) {
+                const int jj = cp - 1;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int64_t row = rt * 16 + rp + e;
+                    const float v = e == 0 ? v2.x : v2.y;
+                    const float ir = e == 0 ? ir0 : ir1;
+                    if (row < a.T) {
+                        if (jj < 2 * N) {
+                            const float sg = ref_sigmoid(v * (ir * alphaPost), a.bias[jj], 0.0f);
+                            a.hPost[row * N + (jj - N)] = sg * 2.0f;
+                        } else {
+                            const float rr = v * (ir * alphaRes);
+                            a.hRes[row * (N * N) + (jj - 2 * N)] = rr + a.bias[jj];
+                        }
+                    }
+                }
+            }
+        };
+        constexpr int PR = M - N;  // hPost + hRes columns
+        static_assert(PR % 4 == 0, "post/res columns in groups of 4 or 8");
+#pragma unroll
+        for (int g0 = 0; g0 < PR; g0 += 8) {
+            if (PR - g0 >= 8) {
+                const float2 v2 = poll_records<8, COLS, 28>(a, tr, N + 1 + g0, lane, tileBase, timedOut);
+                post_res(v2, N + 1 + g0, 8);
+            } else {
+                const float2 v2 = poll_records<4, COLS, 28>(a, tr, N + 1 + g0, lane, tileBase, timedOut);
+                post_res(v2, N + 1 + g0, 4);
+            }
+        }
+    }
+}
+
+template <int N, bool kBf16>
+__global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
+{
+    using S = Shape<N>;
+    constexpr int M = S::M;
+    constexpr int NT = S::NT;
+    using CL = ColLayout<M>;
+    using RC = Rec<N>;
+    constexpr int Q = CL::Q;
+    constexpr int L = kRing;
+    constexpr int E = kLag;
+    constexpr int DP = kPollAhead;
+    constexpr int KS = 2 * N;  // 32-column k-steps per wave (two per stream)
+    static_assert(N == 4, "the strip path keeps the B operand of n = 4 in registers");
+    __shared__ __attribute__((aligned(16))) float part[2][kWaves][RC::COLS * 16];
+    // B operand of each wave's strip, in MFMA fragment order (24 KB per wave).
+    __shared__ u32x4_t bsh[kWaves][KS][NT][64];
+
+    const int g = blockIdx.x;
+    const int xcd = g % a.nXcd;
+    const int j = g / a.nXcd;
+    const int teamSize = a.P + a.R;
+    const int tj = j / teamSize;
+    if (tj >= a.teamsPerXcd) {
+        return;  // spare workgroup: the whole workgroup leaves together
+    }
+    const int team = xcd + a.nXcd * tj;
+    const int role = j % teamSize;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) wave index
+    const int64_t numTeams = a.numTeams;
+    const int64_t ntiles = team < a.RT ? (a.RT - team + numTeams - 1) / numTeams : 0;
+
+    if (role >= a.P) {
+        reducer_role<N>(a, team, ntiles, (role - a.P) * kWaves + w, a.R * kWaves, lane);
+        return;
+    }
+
+    // ---- slice workgroup ----
+    const int p = role;
+    const int Ki = (int)a.K;
+    const int Di = (int)a.D;
+    const int col0 = p * kSlice + w * kStripCols;
+    const int lrow = lane & 7;
+    const int lineOff = 8 * (lane >> 4) + 32 * ((lane >> 3) & 1);
+    const int xLane = (lrow * Ki + col0 + lineOff) * 2;
+    const int hLane = (lrow * Di + col0 + lineOff) * 2;
+    const int rl = lane & 15;
+    const int grp = lane >> 4;
+    const uint32_t epoch = a.epoch;
+
+    if (ntiles == 0) {
+        return;
+    }
+    auto tile_of = [&](int64_t k) { return (int64_t)team + numTeams * k; };
+    // Valid rows of step k's tile; 0 past the team's last tile.
+    auto rows_of = [&](int64_t k) {
+        return k < ntiles ? (int)min((int64_t)16, a.T - tile_of(k) * 16) : 0;
+    };
+
+    // x of a tile goes through a buffer resource based at the tile's first
+    // row and sized to its valid rows: loads past T (or of a step past the
+    // last tile, size 0) read zero without touching memory.  The whole
+    // offset is in the VGPR operand, which the range check covers.
+    u32x4_t xb[L][N][2];
+    auto load_tile = [&](u32x4_t (&dst)[N][2], int64_t k) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(a.x + tile_of(k) * 16 * a.K, rows_of(k) * Ki * 2);
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                dst[s][h] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, xLane + (8 * h * Ki + s * Di) * 2,
+                                                                   0, kCpolNt));
+            }
+        }
+    };
+    // The ring: slot k mod L holds tile k.  Tiles 0 .. L-E-1 are loaded here
+    // and step k < E loads tile k - E + L, so the ring fills over the first E
+    // steps (the slots are zeroed so that the discarded hIn of those steps
+    // reads defined values).
+#pragma unroll
+    for (int b = 0; b < L; ++b) {
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+            xb[b][s][0] = u32x4_t{0u, 0u, 0u, 0u};
+            xb[b][s][1] = u32x4_t{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < L - E; ++b) {
+        load_tile(xb[b], b);
+    }
+
+    // B operand of this wave's strip: fragment (ks, ct) holds, for lane l,
+    // B[k = s*D + col0 + 32q + 8(l/16) + e][slot 16ct + l%16], e = 0..7, with
+    // ks = 2s + q.
+    u32x4_t (*bfr)[NT][64] = bsh[w];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int s = ks >> 1;
+        const int q = ks & 1;
+        const int64_t k0 = (int64_t)s * a.D + col0 + 32 * q + 8 * grp;
+        f32x4_t gm0 = f32x4_t{1.f, 1.f, 1.f, 1.f}, gm1 = gm0;
+        if (a.gamma != nullptr) {
+            gm0 = *reinterpret_cast<const f32x4_t *>(a.gamma + k0);
+            gm1 = *reinterpret_cast<const f32x4_t *>(a.gamma + k0 + 4);
+        }
+#pragma unroll
+        for (int ct = 0; ct < NT; ++ct) {
+            bool lo;
+            int jc;
+            CL::slot(16 * ct + rl, lo, jc);
+            const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)jc * a.K + k0);
+            const f32x4_t ph0 = src[0];
+            const f32x4_t ph1 = src[1];
+            float out[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float bv = e < 4 ? ph0[e] : ph1[e - 4];
+                if (a.gamma != nullptr) {
+                    bv = bv * (e < 4 ? gm0[e] : gm1[e - 4]);
+                }
+                const float hi = bf16_bits_to_f32(f32_to_bf16_bits(bv));
+                out[e] = lo ? (bv - hi) : hi;
+            }
+            bfr[ks][ct][lane] = pack8_bf16(out);
+        }
+    }
+
+    // Every step issues the same memory operations in the same order (8 x
+    // loads, one broadcast poll, one record store and two hIn stores per
+    // lane), whatever the step: out-of-range tiles go through size-0
+    // resources and polls of out-of-range tiles re-read the team's first
+    // block and are ignored.  With no data-dependent branch around a memory
+    // operation, the compiler's wait counts stay exact and no wait drains the
+    // ring.
+    constexpr int NPR = 4;  // broadcast polls in flight: slot k mod 4 for tile k's hIn
+    static_assert(DP + 1 <= NPR && L % NPR == 0, "poll slots");
+    uint64_t pr[NPR];
+#pragma unroll
+    for (int b = 0; b < NPR; ++b) {
+        pr[b] = 0;
+    }
+    const __amdgpu_buffer_rsrc_t bcastAll = make_rsrc(a.bcast, (int)(a.RT * RC::BWORDS * 8));
+    bool timedOut = false;
+
+    for (int64_t k0 = 0; k0 < ntiles + E; k0 += L) {
+#pragma unroll
+        for (int b = 0; b < L; ++b) {
+            const int64_t k = k0 + b;
+            const int64_t rt = tile_of(k);
+            // 1. GEMM of tile k (zeros past the last tile) and its Gram matrix.
+            f32x4_t acc[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+            f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            // B fragments come from LDS, those of the next k-step read while
+            // this step's MFMAs run.
+            u32x4_t bcur[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                bcur[t] = bfr[0][t][lane];
+            }
+#pragma unroll
+            for (int s = 0; s < N; ++s) {
+                u32x4_t kf[2];
+                lines_to_frags(xb[b][s][0], xb[b][s][1], kf[0], kf[1]);
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int ks = 2 * s + q;
+                    u32x4_t bnext[NT];
+                    if (ks + 1 < KS) {
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) {
+                            bnext[t] = bfr[ks + 1][t][lane];
+                        }
+                    }
+                    if constexpr (kBf16) {
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) {
+                            acc[t] = mfma16(kf[q], bcur[t], acc[t]);
+                        }
+                        gram = mfma16(kf[q], kf[q], gram);
+                    } else {
+                        gram = mfma16_f16(kf[q], kf[q], gram);
+                        float f[8];
+                        unpack8<kBf16>(kf[q], f);
+                        u32x4_t ahi, alo;
+                        split_f16_to_bf16(f, ahi, alo);
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) {
+                            acc[t] = mfma16(ahi, bcur[t], acc[t]);
+                            if (CL::has_hi(t)) {
+                                acc[t] = mfma16(alo, bcur[t], acc[t]);
+                            }
+                        }
+                    }
+                    if (ks + 1 < KS) {
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) {
+                            bcur[t] = bnext[t];
+                        }
+                    }
+                }
+            }
+            // Gram diagonal: row r sits in lane 16(r/4) + r, register r % 4.
+            const int di = rl & 3;
+            const float ss = di == 0 ? gram[0] : di == 1 ? gram[1] : di == 2 ? gram[2] : gram[3];
+
+            // 2. This wave's partials into LDS, [column][row]: the C fragment
+            //    gives lane (rl, grp) rows 4grp .. 4grp+3 of column slot 16t + rl.
+            float *mine = &part[b & 1][w][0];
+#pragma unroll
+            for (int t = 0; t < Q; ++t) {
+                const f32x4_t v = acc[t] + acc[Q + t];
+                *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * t + rl) * 16 + 4 * grp) = v;
+            }
+            if constexpr (CL::kHalfTile) {
+                f32x4_t o;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    o[i] = __shfl_xor(acc[2 * Q][i], 8);
+                }
+                if (rl < 8) {
+                    *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * Q + rl) * 16 + 4 * grp) =
+                        acc[2 * Q] + o;
+                }
+            }
+            if ((rl >> 2) == grp) {
+                mine[N * 16 + rl] = ss;
+            }
+            lds_barrier();
+            //    The slice's record: 16-byte chunk tid = (column tid/8, rows
+            //    2(tid%8), +1), the four waves summed in wave order; 8 lanes
+            //    fill one column's 128-byte line.  Lanes past the record and
+            //    steps past the last tile store out of range (dropped).  The
+            //    store itself is issued at the end of the step (below).
+            u32x4_t recw;
+            {
+                const int ch = tid < RC::CHUNKS ? tid : 0;
+                const int c = ch >> 3;
+                const int r0 = 2 * (ch & 7);
+                float2 v = *reinterpret_cast<const float2 *>(&part[b & 1][0][c * 16 + r0]);
+#pragma unroll
+                for (int ww = 1; ww < kWaves; ++ww) {
+                    const float2 u = *reinterpret_cast<const float2 *>(&part[b & 1][ww][c * 16 + r0]);
+                    v.x = v.x + u.x;
+                    v.y = v.y + u.y;
+                }
+                const uint32_t pos = (uint32_t)((rt * a.P + p) * RC::WORDS) + (uint32_t)(c * 16 + r0);
+                recw[0] = __float_as_uint(v.x);
+                recw[1] = rec_tag(pos, epoch);
+                recw[2] = __float_as_uint(v.y);
+                recw[3] = rec_tag(pos + 1u, epoch);
+            }
+
+            // 3. hIn of tile kh = k - E from ring slot hb (static after
+            //    unrolling), with hPre from the poll issued DP steps ago.
+            const int64_t kh = k - E;
+            const int hb = (b - E + 2 * L) % L;
+            const bool liveH = kh >= 0 && kh < ntiles;
+            const int64_t rth = tile_of(kh);
+            uint64_t wv = pr[hb % NPR];
+            const uint32_t want = bcast_tag((uint32_t)(rth * RC::BWORDS) + (uint32_t)lane, epoch);
+            if (liveH && !timedOut && !__all((uint32_t)(wv >> 32) == want)) {
+                const uint64_t *blk = a.bcast + rth * RC::BWORDS;
+                for (uint32_t spins = 0;; ++spins) {
+                    __builtin_amdgcn_s_sleep(1);
+                    wv = ld_word(blk + lane);
+                    if (__all((uint32_t)(wv >> 32) == want)) {
+                        break;
+                    }
+                    if (spins >= a.spinLimit) {
+                        record_timeout(a, lane);
+                        timedOut = true;
+                        break;
+                    }
+                }
+            }
+            // Lane l holds hPre column l/16 of row l%16.
+            const float preC = __uint_as_float((uint32_t)wv);
+            float pre[2][N];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int s = 0; s < N; ++s) {
+                    pre[h][s] = __shfl(preC, 16 * s + 8 * h + lrow);
+                }
+            }
+            u32x4_t hout[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float hv[8];
+#pragma unroll
+                for (int s = 0; s < N; ++s) {
+                    float f[8];
+                    unpack8<kBf16>(xb[hb][s][h], f);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float prod = pre[h][s] * f[e];
+                        hv[e] = (s == 0) ? prod : hv[e] + prod;
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    hout[h][q] = f32_to_x<kBf16>(hv[2 * q]) | (f32_to_x<kBf16>(hv[2 * q + 1]) << 16);
+                }
+            }
+
+            // 4. Memory operations of the step, in this order: the loads of
+            //    tile kh + L into the registers just consumed, the hIn
+            //    stores, the record store, and the poll of the block whose hIn
+            //    runs DP steps from now (the team's first block when that tile
+            //    does not exist).  A wave's vector memory operations retire
+            //    in issue order, so a store whose acknowledgement is slow (the
+            //    device-scope record) delays only the waits for operations
+            //    issued after it; issued last, it has several steps to retire
+            //    before any x load queued behind it is needed.
+            __builtin_amdgcn_sched_barrier(0);
+            load_tile(xb[hb], kh + L);
+            __builtin_amdgcn_sched_barrier(0);
+            {
+                const __amdgpu_buffer_rsrc_t hr =
+                    make_rsrc(a.hIn + rth * 16 * a.D, liveH ? rows_of(kh) * Di * 2 : 0);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    store16<kCpolNt>(hout[h], hr, hLane + 8 * h * Di * 2);
+                }
+                const int recBytes = k < ntiles ? RC::WORDS * 8 : 0;
+                store16<kCpolDev>(recw, make_rsrc(a.recs + (rt * a.P + p) * RC::WORDS, recBytes),
+                                  tid < RC::CHUNKS ? 16 * tid : RC::WORDS * 8);
+                const int64_t kp = kh + DP;
+                const int pb = (hb + DP) % NPR;
+                const int64_t kpc = (kp >= 0 && kp < ntiles) ? kp : 0;
+                pr[pb] = __builtin_bit_cast(
+                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                  bcastAll, (int)((tile_of(kpc) * RC::BWORDS + lane) * 8), 0, kCpolDev));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+template <int N, bool kBf16>
+int strip_coresident_t(int numCUs)
+{
+    int perCU = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &perCU, reinterpret_cast<const void *>(&strip_kernel<N, kBf16>), kWaves * 64, 0) !=
+        hipSuccess) {
+        return -1;
+    }
+    return perCU * numCUs;
+}
+
+template <int N, bool kBf16>
+hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t epoch, hipStream_t stream)
+{
+    char *ws = static_cast<char *>(workspace);
+    StripArgs a;
+    a.x = static_cast<const uint16_t *>(p.x);
+    a.phi = p.phi;
+    a.gamma = p.hasGamma ? p.gamma : nullptr;
+    a.alpha = p.alpha;
+    a.bias = p.bias;
+    a.hIn = static_cast<uint16_t *>(p.hIn);
+    a.hPost = p.hPost;
+    a.hRes = p.hRes;
+    a.hPre = p.hasHPre ? p.hPre : nullptr;
+    a.status = reinterpret_cast<uint64_t *>(ws);
+    a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsFinal);
+    a.recs = reinterpret_cast<uint64_t *>(ws + p.wsFusedPartial);
+    a.T = p.T;
+    a.D = p.D;
+    a.K = p.K;
+    a.RT = p.fusedTiles;
+    a.P = p.stripP;
+    a.R = p.stripR;
+    a.nXcd = p.stripXcds;
+    a.teamsPerXcd = p.stripTeamsPerXcd;
+    a.numTeams = p.stripXcds * p.stripTeamsPerXcd;
+    a.normEps = p.normEps;
+    a.hcEps = p.hcEps;
+    a.invFlatDim = p.invFlatDim;
+    a.epoch = epoch;
+    a.spinLimit = 1u << 20;  // about a second of polling per wait
+    hipLaunchKernelGGL((strip_kernel<N, kBf16>), dim3((unsigned)p.stripGrid), dim3(kWaves * 64), 0,
+                       stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_strip(const Plan &p, void *workspace, uint32_t epoch, hipStream_t stream)
+{
+    if (p.n != 4) {
+        return hipErrorNotSupported;
+    }
+    return p.isBf16 ? launch_strip_t<4, true>(p, workspace, epoch, stream)
+                    : launch_strip_t<4, false>(p, workspace, epoch, stream);
+}
+
+int strip_max_coresident(const Plan &p, int numCUs)
+{
+    if (p.n != 4) {
+        return -1;
+    }
+    return p.isBf16 ? strip_coresident_t<4, true>(numCUs) : strip_coresident_t<4, false>(numCUs);
+}
+
+}  // namespace mhc

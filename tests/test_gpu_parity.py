@@ -84,7 +84,7 @@ def check(out, ref, x_bits, is_bf16, orc):
 
 
 @pytest.mark.parametrize("cfg,force", [(1, None), (2, None), (4, None), (1, "split"),
-                                       (2, "split")])
+                                       (2, "split"), (1, "fused"), (2, "fused")])
 def test_config_full_parity(pkg, orc, device, cfg, force):
     case = CONFIGS[cfg]
     _say(f"[parity] config {cfg} force={force}: {case}")
@@ -100,8 +100,9 @@ def test_cooperative_launch_matches(pkg, orc, device):
     case = CONFIGS[2]
     _say(f"[parity] config 2 cooperative launch: {case}")
     x, phi, alpha, bias, gamma = make_case(case)
-    coop = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, launch="cooperative")
-    plain = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma)
+    coop = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, launch="cooperative",
+                   force_path="fused")
+    plain = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, force_path="fused")
     assert coop["path"] == plain["path"] == "fused"
     for k in ("h_in", "h_post", "h_res", "h_pre"):
         assert np.array_equal(coop[k], plain[k]), k
@@ -242,10 +243,13 @@ def test_determinism(pkg, device):
     op.close()
 
 
-def test_shared_workspace_back_to_back(pkg, orc, device):
+@pytest.mark.parametrize("force,expect", [(None, "strip"), ("fused", "fused")])
+def test_shared_workspace_back_to_back(pkg, orc, device, force, expect):
     """Two executors with different inputs launched back to back on ONE
     workspace: nothing from the first launch (exchange records, published
-    hPre, counters) may leak into the second."""
+    hPre) may leak into the second."""
+    import os
+
     import torch
 
     T, n, D = 400, 4, 7168
@@ -260,12 +264,17 @@ def test_shared_workspace_back_to_back(pkg, orc, device):
         bias = rng.uniform(-0.1, 0.1, M).astype(np.float32)
         gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
         xt, pt, at, bt, gt = to_device(pkg, device, x, True, phi, alpha, bias, gamma)
-        op = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True, workspace=ws)
+        if force is not None:
+            os.environ["MHCPRE_FORCE_PATH"] = force
+        try:
+            op = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True, workspace=ws)
+        finally:
+            os.environ.pop("MHCPRE_FORCE_PATH", None)
         ws = op.workspace
         ops.append(op)
         refs.append(orc.mhc_pre(x, True, phi, alpha, bias, gamma))
         xs.append(x)
-    assert ops[0].path == "fused"
+    assert ops[0].path == expect
     for _ in range(2):
         for op in ops:
             op.launch()

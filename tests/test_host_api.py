@@ -158,7 +158,7 @@ def test_launch_rejects_bad_workspace_before_any_device_work(pkg, lib):
     assert lib.mhcPre(ctypes.c_void_p(FAKE), ws, None, None) == 1
     name = ctypes.c_char_p()
     assert lib.mhcPreExecutorPath(exe, ctypes.byref(name)) == 0
-    assert name.value in (b"split", b"fused")
+    assert name.value in (b"split", b"fused", b"strip")
     assert lib.mhcPreExecutorDestroy(exe) == 0
     assert lib.mhcPreExecutorDestroy(None) == 1
 
