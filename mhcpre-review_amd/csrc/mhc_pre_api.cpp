@@ -258,8 +258,9 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             }
         }
     }
-    // Strip path (n = 4): slices of 256 columns.
-    if (n == 4 && (D % 256) == 0) {
+    // Strip path (n = 4): slices of 256 columns; its tile and row indices are
+    // 32-bit, which bounds T.
+    if (n == 4 && (D % 256) == 0 && T < (int64_t{1} << 24)) {
         p.stripP = static_cast<int>(D / 256);
     }
     p.path = p.stripP > 0 ? mhc::Path::kStrip

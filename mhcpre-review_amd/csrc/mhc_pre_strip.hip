@@ -60,13 +60,15 @@ namespace {
 
 using namespace dev;
 
-constexpr int kWaves = 4;                   // waves per workgroup, one per SIMD
-constexpr int kStripCols = 64;              // x columns of each stream per wave
-constexpr int kSlice = kWaves * kStripCols; // columns per slice
-constexpr int kRing = 8;                    // L: x tiles held per wave
-constexpr int kLag = 5;                     // E: hIn of tile k runs at step k + E
-constexpr int kPollAhead = 2;               // DP: broadcast poll issued DP steps before use
-static_assert(kLag < kRing && kPollAhead <= kLag, "ring geometry");
+constexpr int kGroups = 3;                   // wave groups per workgroup (waves per SIMD)
+constexpr int kStrips = 4;                   // 64-column strips per slice
+constexpr int kWaves = kGroups * kStrips;    // waves per workgroup
+constexpr int kStripCols = 64;               // x columns of each stream per strip
+constexpr int kSlice = kStrips * kStripCols; // columns per slice
+constexpr int kRing = 3;                     // L: x tiles held per wave
+constexpr int kLag = 2;                      // E: hIn of own tile j at own step j + E
+static_assert(kLag < kRing, "ring geometry");
+constexpr int kXccIdReg = (3 << 11) | 20;    // s_getreg operand: HW_REG_XCC_ID, bits [3:0]
 
 struct StripArgs {
     const uint16_t *x;
@@ -285,7 +287,7 @@ __device__ __forceinline__ f32x4_t mfma16_f16(const u32x4_t &a, const u32x4_t &b
 // Reducer wave: the team's steps k = rw, rw + nrw, ...
 template <int N>
 __device__ __forceinline__ void reducer_role(const StripArgs &a, int team, int64_t ntiles, int rw,
-                                             int nrw, int lane)
+                                             int nrw, int lane, bool local)
 {
     using RC = Rec<N>;
     constexpr int M = RC::M;
@@ -354,8 +356,12 @@ __device__ __forceinline__ void reducer_role(const StripArgs &a, int team, int64
                     a.hPre[row * N + c] = v;
                 }
             }
-            store16<kCpolDev>(wv, make_rsrc(a.bcast + rt * RC::BWORDS, RC::BWORDS * 8),
-                              (c * 16 + r0) * 8);
+            const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bcast + rt * RC::BWORDS, RC::BWORDS * 8);
+            if (local) {
+                store16<0>(wv, br, (c * 16 + r0) * 8);
+            } else {
+                store16<kCpolDev>(wv, br, (c * 16 + r0) * 8);
+            }
         }
 
         // hPost / hRes: record columns N+1 .. M (mix columns N .. M-1), up to
@@ -409,12 +415,14 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     constexpr int Q = CL::Q;
     constexpr int L = kRing;
     constexpr int E = kLag;
-    constexpr int DP = kPollAhead;
-    constexpr int KS = 2 * N;  // 32-column k-steps per wave (two per stream)
-    static_assert(N == 4, "the strip path keeps the B operand of n = 4 in registers");
-    __shared__ __attribute__((aligned(16))) float part[2][kWaves][RC::COLS * 16];
-    // B operand of each wave's strip, in MFMA fragment order (24 KB per wave).
-    __shared__ u32x4_t bsh[kWaves][KS][NT][64];
+    constexpr int KS = 2 * N;  // 32-column k-steps per strip (two per stream)
+    static_assert(N == 4, "the strip path is built for n = 4");
+    // Partials of the four strips of each group, double-buffered by own step.
+    __shared__ __attribute__((aligned(16))) float part[kGroups][2][kStrips][RC::COLS * 16];
+    // B operand of each strip, in MFMA fragment order (24 KB per strip).
+    __shared__ u32x4_t bsh[kStrips][KS][NT][64];
+    // Per-group count of partials written (4 per own step).
+    __shared__ uint32_t arrived[kGroups];
 
     const int g = blockIdx.x;
     const int xcd = g % a.nXcd;
@@ -431,17 +439,29 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) wave index
     const int64_t numTeams = a.numTeams;
     const int64_t ntiles = team < a.RT ? (a.RT - team + numTeams - 1) / numTeams : 0;
+    // Exchange stores stay in this XCD's L2 (plain stores, which the readers'
+    // device-scope loads see there) when the workgroup runs on the XCD its
+    // team belongs to; a workgroup placed on another XCD writes through to
+    // memory (sc1).  The hardware dispatches workgroup g to XCD g mod X, so
+    // in practice every store is local.
+    const bool local = a.nXcd > 1 && (int)(__builtin_amdgcn_s_getreg(kXccIdReg) & 15) == xcd;
 
     if (role >= a.P) {
-        reducer_role<N>(a, team, ntiles, (role - a.P) * kWaves + w, a.R * kWaves, lane);
+        reducer_role<N>(a, team, ntiles, (role - a.P) * kWaves + w, a.R * kWaves, lane, local);
         return;
     }
 
     // ---- slice workgroup ----
+    // Wave w: strip w % 4 of the slice, group w / 4.  Group g takes the
+    // team's steps k = g, g + G, g + 2G, ... (its own steps jj = 0, 1, ...),
+    // so the G waves on a SIMD work on different tiles and one computes while
+    // the others wait for the memory queue.
     const int p = role;
+    const int strip = w & 3;
+    const int half = w >> 2;  // the wave's group
     const int Ki = (int)a.K;
     const int Di = (int)a.D;
-    const int col0 = p * kSlice + w * kStripCols;
+    const int col0 = p * kSlice + strip * kStripCols;
     const int lrow = lane & 7;
     const int lineOff = 8 * (lane >> 4) + 32 * ((lane >> 3) & 1);
     const int xLane = (lrow * Ki + col0 + lineOff) * 2;
@@ -449,14 +469,43 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const int rl = lane & 15;
     const int grp = lane >> 4;
     const uint32_t epoch = a.epoch;
-
+    if (tid < kGroups) {
+        arrived[tid] = 0;
+    }
     if (ntiles == 0) {
         return;
     }
-    auto tile_of = [&](int64_t k) { return (int64_t)team + numTeams * k; };
-    // Valid rows of step k's tile; 0 past the team's last tile.
-    auto rows_of = [&](int64_t k) {
-        return k < ntiles ? (int)min((int64_t)16, a.T - tile_of(k) * 16) : 0;
+    // 32-bit tile and row indices (the launch validates T < 2^31 / 16);
+    // byte offsets of a tile are formed in 64 bits from them.
+    const int T32 = (int)a.T;
+    // The kernel arguments the loop uses, as independent scalars: the
+    // compiler otherwise keeps the argument block as one 16-register tuple
+    // and spills and reloads it whole.
+    const char *xBase = reinterpret_cast<const char *>(a.x);
+    char *hBase = reinterpret_cast<char *>(a.hIn);
+    uint64_t *recsBase = a.recs;
+    uint64_t *bcastBase = a.bcast;
+    uint64_t *statusW = a.status;
+    int P32 = a.P;
+    uint32_t spinLimit = a.spinLimit;
+    asm volatile("" : "+s"(xBase), "+s"(hBase), "+s"(recsBase), "+s"(bcastBase), "+s"(statusW),
+                 "+s"(P32), "+s"(spinLimit));
+    const int nt32 = (int)ntiles;
+    const int nmine = (nt32 - half + kGroups - 1) / kGroups;
+    const int teamI = team;
+    const int nTeams = (int)numTeams;
+    const uint32_t xTileBytes = 16u * (uint32_t)Ki * 2u;
+    const uint32_t hTileBytes = 16u * (uint32_t)Di * 2u;
+    // Team tile of own step jj, and its valid rows (0 past the last one).
+    auto tile_of = [&](int jj) { return teamI + nTeams * (kGroups * jj + half); };
+    auto rows_of = [&](int jj) {
+        return (jj >= 0 && jj < nmine) ? min(16, T32 - tile_of(jj) * 16) : 0;
+    };
+    auto x_tile = [&](int jj) {
+        return xBase + (uint64_t)(uint32_t)tile_of(jj) * xTileBytes;
+    };
+    auto h_tile = [&](int jj) {
+        return hBase + (uint64_t)(uint32_t)tile_of(jj) * hTileBytes;
     };
 
     // x of a tile goes through a buffer resource based at the tile's first
@@ -464,22 +513,6 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     // last tile, size 0) read zero without touching memory.  The whole
     // offset is in the VGPR operand, which the range check covers.
     u32x4_t xb[L][N][2];
-    auto load_tile = [&](u32x4_t (&dst)[N][2], int64_t k) {
-        const __amdgpu_buffer_rsrc_t r = make_rsrc(a.x + tile_of(k) * 16 * a.K, rows_of(k) * Ki * 2);
-#pragma unroll
-        for (int s = 0; s < N; ++s) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                dst[s][h] = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, xLane + (8 * h * Ki + s * Di) * 2,
-                                                                   0, kCpolNt));
-            }
-        }
-    };
-    // The ring: slot k mod L holds tile k.  Tiles 0 .. L-E-1 are loaded here
-    // and step k < E loads tile k - E + L, so the ring fills over the first E
-    // steps (the slots are zeroed so that the discarded hIn of those steps
-    // reads defined values).
 #pragma unroll
     for (int b = 0; b < L; ++b) {
 #pragma unroll
@@ -488,17 +521,28 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             xb[b][s][1] = u32x4_t{0u, 0u, 0u, 0u};
         }
     }
+    // The ring: slot jj mod L holds own tile jj.  Tiles 0 .. L-E-1 are loaded
+    // here; step jj loads tile jj - E + L.
 #pragma unroll
     for (int b = 0; b < L - E; ++b) {
-        load_tile(xb[b], b);
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(x_tile(b), rows_of(b) * Ki * 2);
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                xb[b][s][h] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, xLane + (8 * h * Ki + s * Di) * 2,
+                                                                   0, kCpolNt));
+            }
+        }
     }
 
-    // B operand of this wave's strip: fragment (ks, ct) holds, for lane l,
-    // B[k = s*D + col0 + 32q + 8(l/16) + e][slot 16ct + l%16], e = 0..7, with
-    // ks = 2s + q.
-    u32x4_t (*bfr)[NT][64] = bsh[w];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    // B operand of each strip, in LDS for the whole launch: fragment (ks, ct)
+    // holds, for lane l, B[k = s*D + col0 + 32q + 8(l/16) + e][slot 16ct +
+    // l%16], e = 0..7, with ks = 2s + q.  The G waves of a strip share the
+    // k-steps (wave of group g builds ks = g, g + G, ...).
+    u32x4_t (*bfr)[NT][64] = bsh[strip];
+    for (int ks = half; ks < KS; ks += kGroups) {
         const int s = ks >> 1;
         const int q = ks & 1;
         const int64_t k0 = (int64_t)s * a.D + col0 + 32 * q + 8 * grp;
@@ -528,30 +572,116 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             bfr[ks][ct][lane] = pack8_bf16(out);
         }
     }
+    __syncthreads();
 
-    // Every step issues the same memory operations in the same order (8 x
-    // loads, one broadcast poll, one record store and two hIn stores per
+    // Every step issues the same memory operations in the same order (two
+    // hIn stores, one broadcast poll, eight x loads, one record store per
     // lane), whatever the step: out-of-range tiles go through size-0
     // resources and polls of out-of-range tiles re-read the team's first
     // block and are ignored.  With no data-dependent branch around a memory
     // operation, the compiler's wait counts stay exact and no wait drains the
-    // ring.
-    constexpr int NPR = 4;  // broadcast polls in flight: slot k mod 4 for tile k's hIn
-    static_assert(DP + 1 <= NPR && L % NPR == 0, "poll slots");
-    uint64_t pr[NPR];
+    // ring.  The poll of step jj serves the hIn of step jj + 1; the x loads
+    // and the record store of step jj are behind it.
+    uint64_t pr[L];  // broadcast polls: slot j mod L for own tile j's hIn
 #pragma unroll
-    for (int b = 0; b < NPR; ++b) {
+    for (int b = 0; b < L; ++b) {
         pr[b] = 0;
     }
-    const __amdgpu_buffer_rsrc_t bcastAll = make_rsrc(a.bcast, (int)(a.RT * RC::BWORDS * 8));
+    const __amdgpu_buffer_rsrc_t bcastAll = make_rsrc(bcastBase, (int)(a.RT * RC::BWORDS * 8));
     bool timedOut = false;
 
-    for (int64_t k0 = 0; k0 < ntiles + E; k0 += L) {
+    for (int j0 = 0; j0 < nmine + E; j0 += L) {
 #pragma unroll
         for (int b = 0; b < L; ++b) {
-            const int64_t k = k0 + b;
-            const int64_t rt = tile_of(k);
-            // 1. GEMM of tile k (zeros past the last tile) and its Gram matrix.
+            // The step index is recomputed from an opaque copy, so that the
+            // per-step addresses are derived in each step rather than
+            // precomputed for all L unrolled steps and held in registers.
+            int jj = j0 + b;
+            asm volatile("" : "+s"(jj));
+            const int rt = tile_of(jj);
+            const int jh = jj - E;
+            const int hb = (b - E + 2 * L) % L;  // ring slot of own tile jh (static after unrolling)
+            const bool liveH = jh >= 0 && jh < nmine;
+            const int rth = tile_of(jh);
+
+            // 1. hIn of own tile jh = jj - E from ring slot hb, with hPre
+            //    from the poll issued in the previous step (first the
+            //    fast path: the poll already carries every tag).
+            uint64_t wv = pr[hb];
+            const uint32_t want = bcast_tag((uint32_t)(rth * RC::BWORDS) + (uint32_t)lane, epoch);
+            if (liveH && !timedOut && !__all((uint32_t)(wv >> 32) == want)) {
+                const uint64_t *blk = bcastBase + (uint32_t)rth * RC::BWORDS;
+                for (uint32_t spins = 0;; ++spins) {
+                    __builtin_amdgcn_s_sleep(1);
+                    wv = ld_word(blk + lane);
+                    if (__all((uint32_t)(wv >> 32) == want)) {
+                        break;
+                    }
+                    if (spins >= spinLimit) {
+                        if (lane == 0) {
+                            __hip_atomic_store(statusW, ((uint64_t)epoch << 32) | kDeviceTimeout,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                        timedOut = true;
+                        break;
+                    }
+                }
+            }
+            // Lane l holds hPre column l/16 of row l%16.
+            const float preC = __uint_as_float((uint32_t)wv);
+            float pre[2][N];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int s = 0; s < N; ++s) {
+                    pre[h][s] = __shfl(preC, 16 * s + 8 * h + lrow);
+                }
+            }
+            u32x4_t hout[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float hv[8];
+#pragma unroll
+                for (int s = 0; s < N; ++s) {
+                    float f[8];
+                    unpack8<kBf16>(xb[hb][s][h], f);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float prod = pre[h][s] * f[e];
+                        hv[e] = (s == 0) ? prod : hv[e] + prod;
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    hout[h][q] = f32_to_x<kBf16>(hv[2 * q]) | (f32_to_x<kBf16>(hv[2 * q + 1]) << 16);
+                }
+            }
+            //    Poll for the hIn of the next step (own tile jh + 1; the
+            //    team's first tile when that does not exist), issued before
+            //    the hIn stores so that the next step's wait for it does not
+            //    also wait for them.
+            {
+                const int jp = jh + 1;
+                const int jpc = (jp >= 0 && jp < nmine) ? jp : 0;
+                pr[(hb + 1) % L] = __builtin_bit_cast(
+                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
+                                  bcastAll, (tile_of(jpc) * RC::BWORDS + lane) * 8, 0, kCpolDev));
+            }
+            {
+                const __amdgpu_buffer_rsrc_t hr = make_rsrc(h_tile(jh), liveH ? rows_of(jh) * Di * 2 : 0);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    store16<kCpolNt>(hout[h], hr, hLane + 8 * h * Di * 2);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+
+            // 2. GEMM of own tile jj (zeros past the last tile) and its Gram
+            //    matrix, one stream at a time; after each stream's MFMAs the
+            //    two loads of that stream of own tile jh + L go out into the
+            //    slot hIn just consumed.
+            const int jn = jh + L;
+            const __amdgpu_buffer_rsrc_t xr = make_rsrc(x_tile(jn), rows_of(jn) * Ki * 2);
             f32x4_t acc[NT];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -559,7 +689,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             }
             f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
             // B fragments come from LDS, those of the next k-step read while
-            // this step's MFMAs run.
+            // this k-step's MFMAs run.
             u32x4_t bcur[NT];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -606,14 +736,22 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                         }
                     }
                 }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    xb[hb][s][h] = __builtin_bit_cast(
+                        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                     xr, xLane + (8 * h * Ki + s * Di) * 2, 0, kCpolNt));
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
             // Gram diagonal: row r sits in lane 16(r/4) + r, register r % 4.
             const int di = rl & 3;
             const float ss = di == 0 ? gram[0] : di == 1 ? gram[1] : di == 2 ? gram[2] : gram[3];
 
-            // 2. This wave's partials into LDS, [column][row]: the C fragment
+            // 3. This wave's partials into LDS, [column][row]: the C fragment
             //    gives lane (rl, grp) rows 4grp .. 4grp+3 of column slot 16t + rl.
-            float *mine = &part[b & 1][w][0];
+            float *mine = &part[half][jj & 1][strip][0];
 #pragma unroll
             for (int t = 0; t < Q; ++t) {
                 const f32x4_t v = acc[t] + acc[Q + t];
@@ -633,112 +771,56 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             if ((rl >> 2) == grp) {
                 mine[N * 16 + rl] = ss;
             }
-            lds_barrier();
-            //    The slice's record: 16-byte chunk tid = (column tid/8, rows
-            //    2(tid%8), +1), the four waves summed in wave order; 8 lanes
-            //    fill one column's 128-byte line.  Lanes past the record and
-            //    steps past the last tile store out of range (dropped).  The
-            //    store itself is issued at the end of the step (below).
-            u32x4_t recw;
+            //    The four strips of this half meet through an LDS counter
+            //    (the other half keeps running): each adds one after its
+            //    partials, then waits for 4 (jj + 1).  A strip writes this
+            //    buffer again two steps later, after the next meeting, by
+            //    which time every strip has read it.
             {
-                const int ch = tid < RC::CHUNKS ? tid : 0;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                if (lane == 0) {  // one count per wave
+                    __hip_atomic_fetch_add(&arrived[half], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                const uint32_t target = 4u * (uint32_t)(jj + 1);
+                while (__hip_atomic_load(&arrived[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                       target) {
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            }
+            // 4. The slice's record: 16-byte chunk c2 = 64 strip + lane
+            //    (column c2/8, rows 2(c2%8), +1), the four strips summed in
+            //    strip order; 8 lanes fill one column's 128-byte line.  Lanes
+            //    past the record and steps past the last tile store out of
+            //    range (dropped).
+            {
+                const int c2 = strip * 64 + lane;
+                const int ch = c2 < RC::CHUNKS ? c2 : 0;
                 const int c = ch >> 3;
                 const int r0 = 2 * (ch & 7);
-                float2 v = *reinterpret_cast<const float2 *>(&part[b & 1][0][c * 16 + r0]);
+                const float *pb = &part[half][jj & 1][0][0];
+                float2 v = *reinterpret_cast<const float2 *>(pb + c * 16 + r0);
 #pragma unroll
-                for (int ww = 1; ww < kWaves; ++ww) {
-                    const float2 u = *reinterpret_cast<const float2 *>(&part[b & 1][ww][c * 16 + r0]);
+                for (int st = 1; st < kStrips; ++st) {
+                    const float2 u = *reinterpret_cast<const float2 *>(pb + st * RC::COLS * 16 + c * 16 + r0);
                     v.x = v.x + u.x;
                     v.y = v.y + u.y;
                 }
-                const uint32_t pos = (uint32_t)((rt * a.P + p) * RC::WORDS) + (uint32_t)(c * 16 + r0);
+                const uint32_t pos = (uint32_t)((rt * P32 + p) * RC::WORDS) + (uint32_t)(c * 16 + r0);
+                u32x4_t recw;
                 recw[0] = __float_as_uint(v.x);
                 recw[1] = rec_tag(pos, epoch);
                 recw[2] = __float_as_uint(v.y);
                 recw[3] = rec_tag(pos + 1u, epoch);
-            }
-
-            // 3. hIn of tile kh = k - E from ring slot hb (static after
-            //    unrolling), with hPre from the poll issued DP steps ago.
-            const int64_t kh = k - E;
-            const int hb = (b - E + 2 * L) % L;
-            const bool liveH = kh >= 0 && kh < ntiles;
-            const int64_t rth = tile_of(kh);
-            uint64_t wv = pr[hb % NPR];
-            const uint32_t want = bcast_tag((uint32_t)(rth * RC::BWORDS) + (uint32_t)lane, epoch);
-            if (liveH && !timedOut && !__all((uint32_t)(wv >> 32) == want)) {
-                const uint64_t *blk = a.bcast + rth * RC::BWORDS;
-                for (uint32_t spins = 0;; ++spins) {
-                    __builtin_amdgcn_s_sleep(1);
-                    wv = ld_word(blk + lane);
-                    if (__all((uint32_t)(wv >> 32) == want)) {
-                        break;
-                    }
-                    if (spins >= a.spinLimit) {
-                        record_timeout(a, lane);
-                        timedOut = true;
-                        break;
-                    }
+                const __amdgpu_buffer_rsrc_t rr = make_rsrc(
+                    recsBase + ((uint64_t)(uint32_t)rt * (uint32_t)P32 + (uint32_t)p) * RC::WORDS,
+                    jj < nmine ? RC::WORDS * 8 : 0);
+                const int off = c2 < RC::CHUNKS ? 16 * c2 : RC::WORDS * 8;
+                if (local) {
+                    store16<0>(recw, rr, off);
+                } else {
+                    store16<kCpolDev>(recw, rr, off);
                 }
-            }
-            // Lane l holds hPre column l/16 of row l%16.
-            const float preC = __uint_as_float((uint32_t)wv);
-            float pre[2][N];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int s = 0; s < N; ++s) {
-                    pre[h][s] = __shfl(preC, 16 * s + 8 * h + lrow);
-                }
-            }
-            u32x4_t hout[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                float hv[8];
-#pragma unroll
-                for (int s = 0; s < N; ++s) {
-                    float f[8];
-                    unpack8<kBf16>(xb[hb][s][h], f);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float prod = pre[h][s] * f[e];
-                        hv[e] = (s == 0) ? prod : hv[e] + prod;
-                    }
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    hout[h][q] = f32_to_x<kBf16>(hv[2 * q]) | (f32_to_x<kBf16>(hv[2 * q + 1]) << 16);
-                }
-            }
-
-            // 4. Memory operations of the step, in this order: the loads of
-            //    tile kh + L into the registers just consumed, the hIn
-            //    stores, the record store, and the poll of the block whose hIn
-            //    runs DP steps from now (the team's first block when that tile
-            //    does not exist).  A wave's vector memory operations retire
-            //    in issue order, so a store whose acknowledgement is slow (the
-            //    device-scope record) delays only the waits for operations
-            //    issued after it; issued last, it has several steps to retire
-            //    before any x load queued behind it is needed.
-            __builtin_amdgcn_sched_barrier(0);
-            load_tile(xb[hb], kh + L);
-            __builtin_amdgcn_sched_barrier(0);
-            {
-                const __amdgpu_buffer_rsrc_t hr =
-                    make_rsrc(a.hIn + rth * 16 * a.D, liveH ? rows_of(kh) * Di * 2 : 0);
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    store16<kCpolNt>(hout[h], hr, hLane + 8 * h * Di * 2);
-                }
-                const int recBytes = k < ntiles ? RC::WORDS * 8 : 0;
-                store16<kCpolDev>(recw, make_rsrc(a.recs + (rt * a.P + p) * RC::WORDS, recBytes),
-                                  tid < RC::CHUNKS ? 16 * tid : RC::WORDS * 8);
-                const int64_t kp = kh + DP;
-                const int pb = (hb + DP) % NPR;
-                const int64_t kpc = (kp >= 0 && kp < ntiles) ? kp : 0;
-                pr[pb] = __builtin_bit_cast(
-                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
-                                  bcastAll, (int)((tile_of(kpc) * RC::BWORDS + lane) * 8), 0, kCpolDev));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
