@@ -286,13 +286,25 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         align_up(splitPartial + static_cast<size_t>(S) * static_cast<size_t>(T) * (M + 1) * 4, 256);
     p.wsBsplit = splitBsplit;
     p.wsPartial = splitPartial;
+    // Fused and strip paths share the two exchange regions: per-tile blocks
+    // and records (fused), or per-team rings of them (strip), whichever is
+    // larger.
     size_t fusedEnd = 0;
     if (p.fusedP > 0) {
+        size_t bcastSlots = static_cast<size_t>(rowTiles);
+        size_t recSlots = static_cast<size_t>(rowTiles);
+        if (p.stripP > 0) {
+            p.stripMaxTeams = static_cast<int>(
+                std::min<int64_t>(rowTiles, std::max(1, 1024 / (p.stripP + 1))));
+            const size_t ring = static_cast<size_t>(p.stripMaxTeams) * mhc::strip_ring_slots();
+            bcastSlots = std::max(bcastSlots, ring);
+            recSlots = std::max(recSlots, ring);
+        }
         p.wsFinal = mhc::kWsHeaderBytes;
-        p.wsFusedPartial = align_up(
-            p.wsFinal + static_cast<size_t>(rowTiles) * mhc::fused_bcast_words(n) * 8, 256);
-        fusedEnd = align_up(p.wsFusedPartial + static_cast<size_t>(rowTiles) * p.fusedP *
-                                                   mhc::fused_record_words(n) * 8, 256);
+        p.wsFusedPartial =
+            align_up(p.wsFinal + bcastSlots * mhc::fused_bcast_words(n) * 8, 256);
+        fusedEnd = align_up(
+            p.wsFusedPartial + recSlots * p.fusedP * mhc::fused_record_words(n) * 8, 256);
     }
     p.wsTotal = std::max(splitEnd, fusedEnd);
     return MHC_STATUS_SUCCESS;
@@ -377,7 +389,12 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
         // One workgroup per CU, all co-resident; each XCD's CUs hold at least
         // one team of stripP slice workgroups and one reducer workgroup.
         const int perXcd = shape.cus / shape.xcds;
-        const int teamsPerXcd = perXcd / (p.stripP + 1);
+        int teamsPerXcd = perXcd / (p.stripP + 1);
+        // Teams beyond the rings' capacity would have no slots of their own
+        // (teams without tiles write nothing).
+        if (teamsPerXcd * shape.xcds > p.stripMaxTeams && p.stripMaxTeams < p.fusedTiles) {
+            teamsPerXcd = p.stripMaxTeams / shape.xcds;
+        }
         if (teamsPerXcd >= 1 && mhc::strip_max_coresident(p, shape.cus) >= shape.cus) {
             mhc::Plan lp = p;
             lp.stripXcds = shape.xcds;

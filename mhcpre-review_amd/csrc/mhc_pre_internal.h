@@ -66,6 +66,7 @@ struct Plan {
     // stripXcds, stripTeamsPerXcd and stripGrid are filled per launch from
     // the device.
     int stripP = 0;
+    int stripMaxTeams = 0;  // teams the workspace's exchange rings are sized for
     int stripR = 0;
     int stripXcds = 0;
     int stripTeamsPerXcd = 0;
@@ -102,6 +103,9 @@ hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t epoch, hipSt
 // Workgroups of the strip kernel that can be resident per CU (x numCUs), or
 // -1 if the plan has no strip kernel.
 int strip_max_coresident(const Plan &plan, int numCUs);
+
+// Exchange ring slots per team of the strip kernel.
+int strip_ring_slots();
 
 // Largest number of fused-path workgroups that can be co-resident on a device
 // with numCUs compute units, or -1 if the plan has no fused kernel.

@@ -60,14 +60,20 @@ namespace {
 
 using namespace dev;
 
-constexpr int kGroups = 3;                   // wave groups per workgroup (waves per SIMD)
+constexpr int kGroups = 2;                   // wave groups per workgroup (waves per SIMD)
 constexpr int kStrips = 4;                   // 64-column strips per slice
 constexpr int kWaves = kGroups * kStrips;    // waves per workgroup
 constexpr int kStripCols = 64;               // x columns of each stream per strip
 constexpr int kSlice = kStrips * kStripCols; // columns per slice
-constexpr int kRing = 3;                     // L: x tiles held per wave
-constexpr int kLag = 2;                      // E: hIn of own tile j at own step j + E
+constexpr int kRing = 4;                     // L: x tiles held per wave
+constexpr int kLag = 3;                      // E: hIn of own tile j at own step j + E
 static_assert(kLag < kRing, "ring geometry");
+// Exchange ring: team step k uses record / broadcast slot k mod kRingSlots.
+// A slice writes step k + kRingSlots's record only after its hIn of step k,
+// that is after reading step k's broadcast block, which the reducer writes
+// only after reading every record of step k; (E + 1) G slots leave one own
+// step of margin.
+constexpr int kRingSlots = (kLag + 1) * kGroups;
 constexpr int kXccIdReg = (3 << 11) | 20;    // s_getreg operand: HW_REG_XCC_ID, bits [3:0]
 
 struct StripArgs {
@@ -80,8 +86,8 @@ struct StripArgs {
     float *hPost;
     float *hRes;
     float *hPre;
-    uint64_t *recs;    // [RT][P] records of Rec<N>::WORDS tagged words
-    uint64_t *bcast;   // [RT] blocks of Rec<N>::BWORDS tagged words
+    uint64_t *recs;    // [team][ringSlots][P] records of Rec<N>::WORDS tagged words
+    uint64_t *bcast;   // [team][ringSlots] blocks of Rec<N>::BWORDS tagged words
     uint64_t *status;  // (epoch << 32) | kDeviceTimeout after a timeout
     int64_t T;
     int64_t D;
@@ -168,100 +174,12 @@ __device__ __forceinline__ void store16(const u32x4_t &v, __amdgpu_buffer_rsrc_t
         __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v), r, off, 0, kCpol);
 }
 
-// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
-// every outstanding global load of the wave, which would drain the x ring.
-__device__ __forceinline__ void lds_barrier()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 __device__ __forceinline__ void record_timeout(const StripArgs &a, int lane)
 {
     if (lane == 0) {
         __hip_atomic_store(a.status, ((uint64_t)a.epoch << 32) | kDeviceTimeout, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
-}
-
-// Sums over the P slice records of a tile, for record columns c0 .. c0+NC-1
-// and all 16 rows, checking every word's tag.  Lane l takes item
-// it = l % (8 NC) (column c0 + it/8, rows 2(it%8) and 2(it%8) + 1, one 16-byte
-// load per slice) and slice group sg = l / (8 NC), and adds slices sg,
-// sg + NSG, ... in increasing order; the groups are then added in order
-// 0, 1, ..., NSG-1, so the result is a fixed-order sum.  Loads are issued U
-// slices per lane at a time.  Lanes it < 8 NC return the two row totals of
-// their item; valid is true when every word read carried the expected tag.
-template <int NC, int COLS, int U>
-__device__ __forceinline__ float2 sum_records(__amdgpu_buffer_rsrc_t r, int c0, int P, int lane,
-                                              uint32_t tileBase, uint32_t epoch, bool &valid)
-{
-    constexpr int NIT = 8 * NC;
-    constexpr int NSG = 64 / NIT;
-    static_assert(NSG >= 1, "at most 8 columns per call");
-    const int it = lane % NIT;
-    const int sg = lane / NIT;
-    const bool act = sg < NSG;
-    const int c = c0 + it / 8;
-    const int row0 = 2 * (it % 8);
-    float2 acc = make_float2(0.f, 0.f);
-    bool ok = true;
-    for (int q0 = 0; q0 < P; q0 += NSG * U) {
-        u32x4_t t[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int q = q0 + sg + NSG * u;
-            t[u] = (act && q < P)
-                       ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         r, ((q * COLS + c) * 16 + row0) * 8, 0,
-                                                         kCpolDev))
-                       : u32x4_t{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int q = q0 + sg + NSG * u;
-            if (act && q < P) {
-                const uint32_t pos = tileBase + (uint32_t)((q * COLS + c) * 16 + row0);
-                ok = ok && t[u][1] == rec_tag(pos, epoch) && t[u][3] == rec_tag(pos + 1u, epoch);
-                acc.x = acc.x + __uint_as_float(t[u][0]);
-                acc.y = acc.y + __uint_as_float(t[u][2]);
-            }
-        }
-    }
-    float2 tot = acc;
-#pragma unroll
-    for (int k = 1; k < NSG; ++k) {
-        tot.x = tot.x + __shfl(acc.x, it + k * NIT);
-        tot.y = tot.y + __shfl(acc.y, it + k * NIT);
-    }
-    valid = __all(ok);
-    return tot;
-}
-
-// sum_records, repeated until every word carries its tag (or the spin limit
-// runs out, which is recorded in the status word).
-// After a wave's first timeout (timedOut set) it no longer waits at all, so
-// a launch whose exchange failed ends after one spin limit per wave.
-template <int NC, int COLS, int U>
-__device__ __forceinline__ float2 poll_records(const StripArgs &a, __amdgpu_buffer_rsrc_t r, int c0,
-                                               int lane, uint32_t tileBase, bool &timedOut)
-{
-    float2 tot;
-    bool valid = false;
-    for (uint32_t spins = 0;; ++spins) {
-        tot = sum_records<NC, COLS, U>(r, c0, a.P, lane, tileBase, a.epoch, valid);
-        if (valid || timedOut) {
-            break;
-        }
-        if (spins >= a.spinLimit) {
-            record_timeout(a, lane);
-            timedOut = true;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(2);
-    }
-    return tot;
 }
 
 // A fragments of k-steps 2q and 2q + 1 from the line-layout registers r0
@@ -284,123 +202,152 @@ __device__ __forceinline__ f32x4_t mfma16_f16(const u32x4_t &a, const u32x4_t &b
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-// Reducer wave: the team's steps k = rw, rw + nrw, ...
+// Reducer workgroup r of a team: the team's steps k = r, r + R, ..., one
+// tile at a time with all its waves.  Thread t takes item t % 200 (record
+// column c = item / 8, rows 2(item % 8) and +1) and slice group t / 200, and
+// sums the records of slices sg, sg + SG, ... in increasing order; the groups
+// are then added in order in LDS, so every sum has a fixed order.  Every word
+// read must carry its tag; the whole workgroup retries until all do.  hPre is
+// published (the broadcast block) only after every column of every record of
+// the tile has been read, so a slice that has seen the block may reuse the
+// tile's ring slot.
 template <int N>
-__device__ __forceinline__ void reducer_role(const StripArgs &a, int team, int64_t ntiles, int rw,
-                                             int nrw, int lane, bool local)
+__device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int ntiles, int r, int R,
+                                           bool local, float *lds)
 {
     using RC = Rec<N>;
     constexpr int M = RC::M;
     constexpr int COLS = RC::COLS;
+    constexpr int ITEMS = COLS * 8;
+    constexpr int SG = (kWaves * 64) / ITEMS;
+    constexpr int U = 16;  // record loads in flight per thread
+    static_assert(SG >= 1 && SG * ITEMS <= kWaves * 64, "reducer layout");
+    float *sums = lds;                    // [SG][ITEMS][2]
+    float *irs = lds + SG * ITEMS * 2;    // [16] invRms per row
+    const int tid = threadIdx.x;
+    const int item = tid % ITEMS;
+    const int sg = tid / ITEMS;
+    const bool act = sg < SG;
+    const int c = item >> 3;
+    const int r0 = 2 * (item & 7);
+    const int P = a.P;
+    const uint32_t epoch = a.epoch;
     const float alphaPre = a.alpha[0];
     const float alphaPost = a.alpha[1];
     const float alphaRes = a.alpha[2];
-    const uint32_t epoch = a.epoch;
-    const int P = a.P;
     bool timedOut = false;
-    for (int64_t k = rw; k < ntiles; k += nrw) {
-        const int64_t rt = (int64_t)team + (int64_t)a.numTeams * k;
-        const __amdgpu_buffer_rsrc_t tr = make_rsrc(a.recs + rt * P * RC::WORDS, P * RC::WORDS * 8);
+    for (int k = r; k < ntiles; k += R) {
+        const int rt = team + a.numTeams * k;
+        const uint32_t slot = (uint32_t)(team * kRingSlots + k % kRingSlots);
+        const __amdgpu_buffer_rsrc_t tr =
+            make_rsrc(a.recs + (uint64_t)slot * P * RC::WORDS, P * RC::WORDS * 8);
         const uint32_t tileBase = (uint32_t)(rt * P * RC::WORDS);
-
-        // Cheap readiness poll first: the last hPre chunk (sum of squares,
-        // rows 14-15) of every slice record, one 16-byte load per lane.
-        {
-            const int cc = N * 16 + 14;
-            for (uint32_t spins = 0;; ++spins) {
-                bool ok = true;
-                if (lane < P) {
-                    const u32x4_t t = __builtin_bit_cast(
-                        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                     tr, (lane * COLS * 16 + cc) * 8, 0, kCpolDev));
-                    const uint32_t pos = tileBase + (uint32_t)(lane * COLS * 16 + cc);
-                    ok = t[1] == rec_tag(pos, epoch) && t[3] == rec_tag(pos + 1u, epoch);
-                }
-                if (__all(ok) || timedOut) {
-                    break;
-                }
-                if (spins >= a.spinLimit) {
-                    record_timeout(a, lane);
-                    timedOut = true;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-            }
-        }
-
-        // hPre mix columns 0..N-1 and the sum of squares (column N).
-        constexpr int NIT = 8 * (N + 1);
-        const float2 tot = poll_records<N + 1, COLS, 32>(a, tr, 0, lane, tileBase, timedOut);
-        const int it = lane % NIT;
-        const int c = it / 8;
-        const int r0 = 2 * (it % 8);
-        // invRms of rows 2(l % 8), 2(l % 8) + 1 in every lane, from the
-        // sum-of-squares lanes 8N + l % 8.
-        const float irA = ref_inv_rms(tot.x, a.invFlatDim, a.normEps);
-        const float irB = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
-        const float ir0 = __shfl(irA, 8 * N + (lane & 7));
-        const float ir1 = __shfl(irB, 8 * N + (lane & 7));
-        if (lane < 8 * N) {
-            const float bc = a.bias[c];
-            u32x4_t wv;
+        float2 acc;
+        for (uint32_t spins = 0;; ++spins) {
+            acc = make_float2(0.f, 0.f);
+            bool ok = true;
+            if (act) {
+                for (int q0 = sg; q0 < P; q0 += SG * U) {
+                    u32x4_t t[U];
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const float ir = e == 0 ? ir0 : ir1;
-                const float mix = e == 0 ? tot.x : tot.y;
-                const float v = ref_sigmoid(mix * (ir * alphaPre), bc, a.hcEps);
-                const int idx = c * 16 + r0 + e;
-                wv[2 * e] = __float_as_uint(v);
-                wv[2 * e + 1] = bcast_tag((uint32_t)(rt * RC::BWORDS) + idx, epoch);
-                const int64_t row = rt * 16 + r0 + e;
-                if (a.hPre != nullptr && row < a.T) {
-                    a.hPre[row * N + c] = v;
-                }
-            }
-            const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bcast + rt * RC::BWORDS, RC::BWORDS * 8);
-            if (local) {
-                store16<0>(wv, br, (c * 16 + r0) * 8);
-            } else {
-                store16<kCpolDev>(wv, br, (c * 16 + r0) * 8);
-            }
-        }
-
-        // hPost / hRes: record columns N+1 .. M (mix columns N .. M-1), up to
-        // 8 columns per pass.
-        auto post_res = [&](const float2 &v2, int cc0, int ncols) {
-            const int itp = lane % (8 * ncols);
-            const int cp = cc0 + itp / 8;
-            const int rp = 2 * (itp % 8);
-            if (lane < 8 * ncols) {
-                const int jj = cp - 1;
+                    for (int u = 0; u < U; ++u) {
+                        const int q = q0 + SG * u;
+                        t[u] = q < P ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                       tr, ((q * COLS + c) * 16 + r0) * 8, 0,
+                                                                       kCpolDev))
+                                     : u32x4_t{0u, 0u, 0u, 0u};
+                    }
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int64_t row = rt * 16 + rp + e;
-                    const float v = e == 0 ? v2.x : v2.y;
-                    const float ir = e == 0 ? ir0 : ir1;
-                    if (row < a.T) {
-                        if (jj < 2 * N) {
-                            const float sg = ref_sigmoid(v * (ir * alphaPost), a.bias[jj], 0.0f);
-                            a.hPost[row * N + (jj - N)] = sg * 2.0f;
-                        } else {
-                            const float rr = v * (ir * alphaRes);
-                            a.hRes[row * (N * N) + (jj - 2 * N)] = rr + a.bias[jj];
+                    for (int u = 0; u < U; ++u) {
+                        const int q = q0 + SG * u;
+                        if (q < P) {
+                            const uint32_t pos = tileBase + (uint32_t)((q * COLS + c) * 16 + r0);
+                            ok = ok && t[u][1] == rec_tag(pos, epoch) && t[u][3] == rec_tag(pos + 1u, epoch);
+                            acc.x = acc.x + __uint_as_float(t[u][0]);
+                            acc.y = acc.y + __uint_as_float(t[u][2]);
                         }
                     }
                 }
             }
-        };
-        constexpr int PR = M - N;  // hPost + hRes columns
-        static_assert(PR % 4 == 0, "post/res columns in groups of 4 or 8");
+            const bool all = __syncthreads_and(ok) != 0;
+            if (all || timedOut) {
+                break;
+            }
+            if (spins >= a.spinLimit) {
+                record_timeout(a, tid);
+                timedOut = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (act) {
+            sums[(sg * ITEMS + item) * 2] = acc.x;
+            sums[(sg * ITEMS + item) * 2 + 1] = acc.y;
+        }
+        __syncthreads();
+        float2 tot = make_float2(0.f, 0.f);
+        if (tid < ITEMS) {
 #pragma unroll
-        for (int g0 = 0; g0 < PR; g0 += 8) {
-            if (PR - g0 >= 8) {
-                const float2 v2 = poll_records<8, COLS, 28>(a, tr, N + 1 + g0, lane, tileBase, timedOut);
-                post_res(v2, N + 1 + g0, 8);
-            } else {
-                const float2 v2 = poll_records<4, COLS, 28>(a, tr, N + 1 + g0, lane, tileBase, timedOut);
-                post_res(v2, N + 1 + g0, 4);
+            for (int g = 0; g < SG; ++g) {
+                tot.x = tot.x + sums[(g * ITEMS + item) * 2];
+                tot.y = tot.y + sums[(g * ITEMS + item) * 2 + 1];
+            }
+            if (c == N) {  // sum of squares: invRms of rows r0, r0 + 1
+                irs[r0] = ref_inv_rms(tot.x, a.invFlatDim, a.normEps);
+                irs[r0 + 1] = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
             }
         }
+        __syncthreads();
+        if (tid < ITEMS && c != N) {
+            const float ir0 = irs[r0];
+            const float ir1 = irs[r0 + 1];
+            if (c < N) {
+                // hPre column c: broadcast words (rows r0, r0 + 1) and the
+                // optional hPre output.
+                const float bc = a.bias[c];
+                u32x4_t wv;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float ir = e == 0 ? ir0 : ir1;
+                    const float mix = e == 0 ? tot.x : tot.y;
+                    const float v = ref_sigmoid(mix * (ir * alphaPre), bc, a.hcEps);
+                    const int idx = c * 16 + r0 + e;
+                    wv[2 * e] = __float_as_uint(v);
+                    wv[2 * e + 1] = bcast_tag((uint32_t)(rt * RC::BWORDS) + idx, epoch);
+                    const int row = rt * 16 + r0 + e;
+                    if (a.hPre != nullptr && row < a.T) {
+                        a.hPre[(int64_t)row * N + c] = v;
+                    }
+                }
+                const __amdgpu_buffer_rsrc_t br =
+                    make_rsrc(a.bcast + (uint64_t)slot * RC::BWORDS, RC::BWORDS * 8);
+                if (local) {
+                    store16<0>(wv, br, (c * 16 + r0) * 8);
+                } else {
+                    store16<kCpolDev>(wv, br, (c * 16 + r0) * 8);
+                }
+            } else {
+                // Mix column j = c - 1 (N .. M-1): hPost or hRes.
+                const int jj = c - 1;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int row = rt * 16 + r0 + e;
+                    const float v = e == 0 ? tot.x : tot.y;
+                    const float ir = e == 0 ? ir0 : ir1;
+                    if (row < a.T) {
+                        if (jj < 2 * N) {
+                            const float sgm = ref_sigmoid(v * (ir * alphaPost), a.bias[jj], 0.0f);
+                            a.hPost[(int64_t)row * N + (jj - N)] = sgm * 2.0f;
+                        } else {
+                            const float rr = v * (ir * alphaRes);
+                            a.hRes[(int64_t)row * (N * N) + (jj - 2 * N)] = rr + a.bias[jj];
+                        }
+                    }
+                }
+            }
+        }
+        static_assert(M - N <= ITEMS, "columns");
+        __syncthreads();  // sums / irs are reused by the next tile
     }
 }
 
@@ -447,7 +394,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const bool local = a.nXcd > 1 && (int)(__builtin_amdgcn_s_getreg(kXccIdReg) & 15) == xcd;
 
     if (role >= a.P) {
-        reducer_role<N>(a, team, ntiles, (role - a.P) * kWaves + w, a.R * kWaves, lane, local);
+        reducer_wg<N>(a, team, (int)ntiles, role - a.P, a.R, local, &part[0][0][0][0]);
         return;
     }
 
@@ -587,7 +534,10 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     for (int b = 0; b < L; ++b) {
         pr[b] = 0;
     }
-    const __amdgpu_buffer_rsrc_t bcastAll = make_rsrc(bcastBase, (int)(a.RT * RC::BWORDS * 8));
+    const __amdgpu_buffer_rsrc_t bcastAll =
+        make_rsrc(bcastBase, a.numTeams * kRingSlots * RC::BWORDS * 8);
+    // Exchange ring slot of own step jj (team step G jj + group).
+    auto slot_of = [&](int jj) { return teamI * kRingSlots + (kGroups * jj + half) % kRingSlots; };
     bool timedOut = false;
 
     for (int j0 = 0; j0 < nmine + E; j0 += L) {
@@ -610,7 +560,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             uint64_t wv = pr[hb];
             const uint32_t want = bcast_tag((uint32_t)(rth * RC::BWORDS) + (uint32_t)lane, epoch);
             if (liveH && !timedOut && !__all((uint32_t)(wv >> 32) == want)) {
-                const uint64_t *blk = bcastBase + (uint32_t)rth * RC::BWORDS;
+                const uint64_t *blk = bcastBase + (uint32_t)slot_of(jh) * RC::BWORDS;
                 for (uint32_t spins = 0;; ++spins) {
                     __builtin_amdgcn_s_sleep(1);
                     wv = ld_word(blk + lane);
@@ -665,7 +615,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 const int jpc = (jp >= 0 && jp < nmine) ? jp : 0;
                 pr[(hb + 1) % L] = __builtin_bit_cast(
                     uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
-                                  bcastAll, (tile_of(jpc) * RC::BWORDS + lane) * 8, 0, kCpolDev));
+                                  bcastAll, (slot_of(jpc) * RC::BWORDS + lane) * 8, 0, kCpolDev));
             }
             {
                 const __amdgpu_buffer_rsrc_t hr = make_rsrc(h_tile(jh), liveH ? rows_of(jh) * Di * 2 : 0);
@@ -813,7 +763,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 recw[2] = __float_as_uint(v.y);
                 recw[3] = rec_tag(pos + 1u, epoch);
                 const __amdgpu_buffer_rsrc_t rr = make_rsrc(
-                    recsBase + ((uint64_t)(uint32_t)rt * (uint32_t)P32 + (uint32_t)p) * RC::WORDS,
+                    recsBase + ((uint64_t)(uint32_t)slot_of(jj) * (uint32_t)P32 + (uint32_t)p) * RC::WORDS,
                     jj < nmine ? RC::WORDS * 8 : 0);
                 const int off = c2 < RC::CHUNKS ? 16 * c2 : RC::WORDS * 8;
                 if (local) {
@@ -885,6 +835,8 @@ hipError_t launch_strip(const Plan &p, void *workspace, uint32_t epoch, hipStrea
     return p.isBf16 ? launch_strip_t<4, true>(p, workspace, epoch, stream)
                     : launch_strip_t<4, false>(p, workspace, epoch, stream);
 }
+
+int strip_ring_slots() { return kRingSlots; }
 
 int strip_max_coresident(const Plan &p, int numCUs)
 {
