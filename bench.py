@@ -5,8 +5,9 @@ Workload (default): the headline prefill shape n=4, D=7168, T=8192, bf16 x,
 gamma on -- one "step" is one MhcPre launch over all T rows with every input
 already resident in HBM.  Prints ONE JSON line.
 
-  value      tokens/s = T / (mean launch time over the timed steps), each launch
-             bracketed by HIP events on the stream it is launched on
+  value      tokens/s = T / (mean launch time): the timed steps are launched
+             back to back between one pair of HIP events recorded on the
+             launch stream
   roofline   algorithmic bytes per launch / mean launch time, against 8 TB/s;
              bytes = x + phi + gamma + bias + alpha + hIn + hPost + hRes, each
              counted once (hPre is not part of the operator contract);
@@ -106,12 +107,11 @@ def cpu_baseline(x, phi, alpha, bias, gamma, bf16: bool, target_s: float) -> dic
 
 def measured_traffic(workload: str, path: str):
     """HBM bytes per launch for this workload from the committed rocprofv3 PMC
-    record (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size), or None."""
-    if path != "fused":
-        return None
+    record (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size) of the
+    kernel path this launch takes, or None."""
     for f in sorted((ROOT / "profiles").glob("*.traffic.json")):
         rec = json.loads(f.read_text())
-        if rec.get("workload") == workload:
+        if rec.get("workload") == workload and rec.get("path") == path:
             return rec
     return None
 
@@ -151,17 +151,31 @@ def main() -> int:
         op.launch(stream)
     torch.cuda.synchronize()
 
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # Timed region: K launches back to back on the launch stream, between one
+    # pair of HIP events recorded on that stream.  (An event pair around each
+    # launch puts a marker between consecutive dispatches, which costs about
+    # 10 us of idle GPU per launch; those per-launch figures come from a
+    # separate pass below and only describe the spread.)
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    for i in range(args.steps):
+    t_start.record(stream)
+    for _ in range(args.steps):
+        op.launch(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    mean_ms = total_ms / args.steps
+
+    n_ev = min(args.steps, 20)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    for i in range(n_ev):
         starts[i].record(stream)
         op.launch(stream)
         ends[i].record(stream)
     torch.cuda.synchronize()
     durs = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))  # ms per launch
-    total_ms = starts[0].elapsed_time(ends[-1])
-    mean_ms = sum(durs) / len(durs)
     status = op.device_status(stream)
     if status != 0:
         print(f"device status {status}", file=sys.stderr)
@@ -198,7 +212,9 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": workload,
                    "n": n, "D": D, "T": T, "gamma": gamma_on, "path": op.path,
-                   "median_us": durs[len(durs) // 2] * 1e3, "min_us": durs[0] * 1e3,
+                   "launch_us": mean_ms * 1e3,
+                   "event_pair_median_us": durs[len(durs) // 2] * 1e3,
+                   "event_pair_min_us": durs[0] * 1e3,
                    "algorithmic_bytes": b_alg,
                    "traffic_source": traffic["summary"] if traffic else None},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
