@@ -1,41 +1,43 @@
 // Strip kernel for gfx950 (n = 4, D % 256 == 0): x is read from HBM once,
-// held in VGPRs in a ring of row tiles, and the cross-workgroup exchange of
-// the K-reduction runs in the shadow of the x stream.
+// held in VGPRs in a ring of row tiles until its hIn is written, and the
+// cross-workgroup exchange of the K-reduction runs in the shadow of the x
+// stream.
 //
-// Teams.  The workgroups of one XCD form teams: P = D / 256 slice workgroups
-// and R reducer workgroups each.  Workgroup g runs on XCD g mod X (the
+// Teams.  The workgroups of one XCD form teams of P = D / 256 slice
+// workgroups and R reducer workgroups.  Workgroup g runs on XCD g mod X (the
 // hardware dispatches workgroups round-robin over the X XCDs), so a team's
-// exchange stays inside one XCD's L2.  The exchange itself uses device-scope
-// accesses, so results do not depend on where a workgroup actually runs;
-// only the speed does.  Team t owns row tiles t, t + numTeams, t + 2 numTeams,
-// ... (16 rows each); its k-th tile is its "step k".
+// exchange stays inside one XCD's L2.  Results do not depend on where a
+// workgroup actually runs (one placed off its team's XCD writes through to
+// memory); only the speed does.  Team t owns row tiles t, t + numTeams, ...
+// (16 rows each); its k-th tile is its "team step k".
 //
-// Slice workgroup p (4 waves, one per SIMD).  Wave w owns the 64-column strip
-// [256p + 64w, 256p + 64w + 64) of every stream: 256 values of K, whose B
-// operand (gamma * phi split into bf16 hi + lo, 3 column tiles x 8 k-steps)
-// it keeps in 96 VGPRs for the whole launch.  x of a tile is 16 rows x 4
-// streams x 64 columns = 8 KB per wave (32 VGPRs), loaded as whole 128-byte
-// lines (register (s, h) holds, in lane l, row 8h + (l & 7) and the 8 columns
-// at 8(l >> 4) + 32((l >> 3) & 1) of stream s) and held in a ring of L tiles.
-// Step k of a wave:
-//   1. MFMA of tile k against the B registers (a DPP row_ror:8 turns a pair
-//      of line registers into the A fragments of two k-steps) and a Gram
-//      MFMA of the same fragments, whose diagonal is the sum of squares;
-//   2. the four waves' partials (M mix columns + sumsq, 16 rows) meet in LDS
-//      and are summed in wave order into the slice's record, which is stored
-//      as tagged words (below) in whole 128-byte lines;
-//   3. hIn of tile k - E from the registers, with hPre from the tile's
-//      broadcast block, polled DP steps earlier;
-//   4. a poll of the broadcast block of tile k - E + DP, then the loads of
-//      tile k - E + L into the registers hIn just freed.
-// So the loads of L - E tiles are in flight ahead of the MFMA while E tiles
-// wait for their hPre.
+// Slice workgroup p (8 waves, two per SIMD).  Wave w owns strip w mod 4, the
+// 64 columns [256p + 64(w mod 4), +64) of every stream (256 values of K),
+// and belongs to wave group w / 4; group g takes the team steps g, g + 2, ...
+// (its "own steps"), so the two waves of a SIMD work on different tiles.  The
+// B operand of each strip (gamma * phi split into bf16 hi + lo, 3 column
+// tiles x 8 k-steps, 24 KB) is built once into LDS.  x of a tile is 16 rows
+// x 4 streams x 64 columns = 8 KB per wave (32 VGPRs), loaded as whole
+// 128-byte lines (register (s, h) holds, in lane l, row 8h + (l & 7) and the
+// 8 columns at 8(l >> 4) + 32((l >> 3) & 1) of stream s) into a ring of L
+// tiles.  Own step j of a wave:
+//   1. hIn of own tile j - E from the ring, with hPre from the tile's
+//      broadcast block, polled one own step earlier; the poll for the next
+//      step; the hIn stores;
+//   2. the MFMAs of own tile j against B (a DPP row_ror:8 turns a pair of
+//      line registers into the A fragments of two k-steps) and a Gram MFMA
+//      of the same fragments, whose diagonal is the sum of squares; after
+//      each stream's MFMAs, the loads of that stream of own tile j - E + L go
+//      out into the registers hIn freed;
+//   3. the four strips' partials (M mix columns + sumsq, 16 rows) meet in LDS
+//      and are summed in strip order into the slice's record, stored as
+//      tagged words (below) in whole 128-byte lines.
+// So L - E tiles are loading ahead of the MFMA while E tiles wait for hPre.
 //
-// Reducer workgroup (4 waves).  Reducer wave i of a team takes the team's
-// steps k = i, i + 4R, ...: it polls the P records of the tile, sums the hPre
-// mix columns and the sum of squares over the slices in slice order,
-// evaluates invRms and hPre, publishes hPre as a broadcast block of tagged
-// words, then sums the hPost / hRes columns and writes those outputs.
+// Reducer workgroup r of a team takes the team steps r, r + R, ...: it polls
+// the P records of the tile, sums them in slice order, evaluates invRms and
+// hPre, publishes hPre as a broadcast block of tagged words, then writes the
+// hPre, hPost and hRes outputs.
 //
 // Exchange words.  Every exchanged value is one 8-byte word: the fp32 bits in
 // the low half and a tag in the high half, written and read as single-copy
@@ -65,7 +67,7 @@ constexpr int kStrips = 4;                   // 64-column strips per slice
 constexpr int kWaves = kGroups * kStrips;    // waves per workgroup
 constexpr int kStripCols = 64;               // x columns of each stream per strip
 constexpr int kSlice = kStrips * kStripCols; // columns per slice
-constexpr int kRing = 4;                     // L: x tiles held per wave
+constexpr int kRing = 5;                     // L: x tiles held per wave
 constexpr int kLag = 3;                      // E: hIn of own tile j at own step j + E
 static_assert(kLag < kRing, "ring geometry");
 // Exchange ring: team step k uses record / broadcast slot k mod kRingSlots.
@@ -154,17 +156,29 @@ __device__ __forceinline__ uint32_t bcast_tag(uint32_t pos, uint32_t epoch)
     return (pos * 0x85EBCA77u) ^ epoch ^ 0xC2B2AE3Du;
 }
 
-__device__ __forceinline__ uint64_t ld_word(const uint64_t *p)
-{
-    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 constexpr int kCpolNt = 2;    // nontemporal: x and hIn are streamed once
 constexpr int kCpolDev = 16;  // sc1: device-scope coherent
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int bytes)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, 0x00020000);
+}
+
+// Every global access of the kernel is a buffer instruction, the exchange
+// words and the status word included (aligned 8-byte accesses, performed as
+// one access, sc1).  Atomics through generic pointers would compile to FLAT
+// instructions, which count on both the vector-memory and the LDS counters:
+// with one of them in flight, every later counter wait of the wave has to
+// wait for zero, which drains the x ring at every step.
+__device__ __forceinline__ uint64_t ld_word(__amdgpu_buffer_rsrc_t r, int off)
+{
+    return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCpolDev));
+}
+__device__ __forceinline__ void st_status(uint64_t *status, uint32_t epoch)
+{
+    const uint64_t v = ((uint64_t)epoch << 32) | kDeviceTimeout;
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, v),
+                                          make_rsrc(status, 8), 0, 0, kCpolDev);
 }
 
 template <int kCpol>
@@ -177,8 +191,7 @@ __device__ __forceinline__ void store16(const u32x4_t &v, __amdgpu_buffer_rsrc_t
 __device__ __forceinline__ void record_timeout(const StripArgs &a, int lane)
 {
     if (lane == 0) {
-        __hip_atomic_store(a.status, ((uint64_t)a.epoch << 32) | kDeviceTimeout, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        st_status(a.status, a.epoch);
     }
 }
 
@@ -560,17 +573,16 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             uint64_t wv = pr[hb];
             const uint32_t want = bcast_tag((uint32_t)(rth * RC::BWORDS) + (uint32_t)lane, epoch);
             if (liveH && !timedOut && !__all((uint32_t)(wv >> 32) == want)) {
-                const uint64_t *blk = bcastBase + (uint32_t)slot_of(jh) * RC::BWORDS;
+                const int blkOff = (slot_of(jh) * RC::BWORDS + lane) * 8;
                 for (uint32_t spins = 0;; ++spins) {
                     __builtin_amdgcn_s_sleep(1);
-                    wv = ld_word(blk + lane);
+                    wv = ld_word(bcastAll, blkOff);
                     if (__all((uint32_t)(wv >> 32) == want)) {
                         break;
                     }
                     if (spins >= spinLimit) {
                         if (lane == 0) {
-                            __hip_atomic_store(statusW, ((uint64_t)epoch << 32) | kDeviceTimeout,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            st_status(statusW, epoch);
                         }
                         timedOut = true;
                         break;
