@@ -258,9 +258,9 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             }
         }
     }
-    // Strip path (n = 4): slices of 256 columns; its tile and row indices are
-    // 32-bit, which bounds T.
-    if (n == 4 && (D % 256) == 0 && T < (int64_t{1} << 24)) {
+    // Strip path (n = 4): slices of 256 columns, at most strip_max_slices()
+    // of them; its tile and row indices are 32-bit, which bounds T.
+    if (n == 4 && (D % 256) == 0 && D / 256 <= mhc::strip_max_slices() && T < (int64_t{1} << 24)) {
         p.stripP = static_cast<int>(D / 256);
     }
     p.path = p.stripP > 0 ? mhc::Path::kStrip
@@ -399,7 +399,8 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
             mhc::Plan lp = p;
             lp.stripXcds = shape.xcds;
             lp.stripTeamsPerXcd = teamsPerXcd;
-            lp.stripR = perXcd / teamsPerXcd - p.stripP;
+            // Workgroups of a team beyond the slices and reducers leave at once.
+            lp.stripR = mhc::strip_reducers(perXcd / teamsPerXcd - p.stripP);
             lp.stripGrid = shape.cus;
             const uint32_t epoch = next_epoch();
             executor->lastEpoch.store(epoch, std::memory_order_relaxed);

@@ -106,6 +106,12 @@ int strip_max_coresident(const Plan &plan, int numCUs);
 
 // Exchange ring slots per team of the strip kernel.
 int strip_ring_slots();
+// Largest number of slice workgroups per team the strip kernel supports.
+int strip_max_slices();
+// Reducer workgroups per team the strip kernel uses when `available` (>= 1)
+// workgroups per team are left over after the slices (1, 2 or 4; the ring
+// size depends on it).
+int strip_reducers(int available);
 
 // Largest number of fused-path workgroups that can be co-resident on a device
 // with numCUs compute units, or -1 if the plan has no fused kernel.

@@ -70,12 +70,21 @@ constexpr int kSlice = kStrips * kStripCols; // columns per slice
 constexpr int kRing = 5;                     // L: x tiles held per wave
 constexpr int kLag = 3;                      // E: hIn of own tile j at own step j + E
 static_assert(kLag < kRing, "ring geometry");
-// Exchange ring: team step k uses record / broadcast slot k mod kRingSlots.
-// A slice writes step k + kRingSlots's record only after its hIn of step k,
-// that is after reading step k's broadcast block, which the reducer writes
-// only after reading every record of step k; (E + 1) G slots leave one own
-// step of margin.
-constexpr int kRingSlots = (kLag + 1) * kGroups;
+// Exchange ring: team step k uses record / broadcast slot k mod S, and the
+// team has R reducers, R in {1, 2, 4} (reducer k mod R takes step k).  A
+// slice of group h writes the record of step m (m = h mod 2) at the end of
+// its own step m / 2, after its hIn of step m - 2E, that is after it has seen
+// the broadcast block of step m - 2E.  That block's reducer publishes it
+// after finishing (both phases of) its previous tile, step m - 2E - R, and
+// every tile before.  The slot's previous occupant, step m - S, is among
+// those when some step m - S + tR (t >= 1, tR even, so of the same group) is
+// at most m - 2E: S = 2E + 4 does it for R = 1, 2 and 4.  The broadcast
+// block of step m is written only after every slice has written the record
+// of step m, hence after each has read the block of step m - S.
+constexpr int kMaxReducers = 4;
+constexpr int kRingSlots = 2 * kLag + kMaxReducers;
+static_assert(kRingSlots >= (kLag + 1) * kGroups, "ring slots");
+constexpr int kMaxSlices = 31;              // slice workgroups per team (the reducer loads are sized for it)
 constexpr int kXccIdReg = (3 << 11) | 20;    // s_getreg operand: HW_REG_XCC_ID, bits [3:0]
 
 struct StripArgs {
@@ -216,74 +225,104 @@ __device__ __forceinline__ f32x4_t mfma16_f16(const u32x4_t &a, const u32x4_t &b
 }
 
 // Reducer workgroup r of a team: the team's steps k = r, r + R, ..., one
-// tile at a time with all its waves.  Thread t takes item t % 200 (record
-// column c = item / 8, rows 2(item % 8) and +1) and slice group t / 200, and
-// sums the records of slices sg, sg + SG, ... in increasing order; the groups
-// are then added in order in LDS, so every sum has a fixed order.  Every word
-// read must carry its tag; the whole workgroup retries until all do.  hPre is
-// published (the broadcast block) only after every column of every record of
-// the tile has been read, so a slice that has seen the block may reuse the
-// tile's ring slot.
+// tile at a time with all its waves, in two phases.
+//   Phase 1 reads record columns 0..N (the hPre mix columns and the sum of
+//   squares): thread t takes item t % (8 (N+1)) (column item / 8, rows
+//   2 (item % 8) and +1) and slice group t / (8 (N+1)), and sums the records
+//   of slices sg, sg + SG1, ... in increasing order.  Every word read must
+//   carry its tag; the whole workgroup retries until all do.  The groups are
+//   then added in order in LDS, invRms and hPre are evaluated, and hPre is
+//   published (the broadcast block).
+//   Phase 2 reads the hPost / hRes columns N+1 .. M the same way (their
+//   loads go out before the hPre arithmetic) and writes those outputs.
+// Every sum has a fixed order.  hPre is published only after every column of
+// every record of the tile has been read by the phase-2 loads issued before
+// it, so a slice that has seen the block may reuse the tile's ring slot.
+template <int N, int C0, int NC, int UMAX>
+struct ColPoll {
+    static constexpr int ITEMS = NC * 8;
+    static constexpr int SG = (kWaves * 64) / ITEMS;
+    static_assert(SG >= 1, "reducer layout");
+    int c, r0, sg;
+    bool act;
+    u32x4_t t[UMAX];
+    __device__ ColPoll(int tid)
+    {
+        const int item = tid % ITEMS;
+        sg = tid / ITEMS;
+        act = sg < SG;
+        c = C0 + (item >> 3);
+        r0 = 2 * (item & 7);
+    }
+    // Issues the loads of this thread's slices sg, sg + SG, ... (at most UMAX).
+    __device__ void issue(__amdgpu_buffer_rsrc_t tr, int P)
+    {
+#pragma unroll
+        for (int u = 0; u < UMAX; ++u) {
+            const int q = sg + SG * u;
+            t[u] = (act && q < P) ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                    tr, ((q * Rec<N>::COLS + c) * 16 + r0) * 8, 0,
+                                                                    kCpolDev))
+                                  : u32x4_t{0u, 0u, 0u, 0u};
+        }
+    }
+    // Sums the loaded words in slice order; false if a tag does not match.
+    __device__ bool sum(uint32_t tileBase, uint32_t epoch, int P, float2 &acc) const
+    {
+        bool ok = true;
+        acc = make_float2(0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < UMAX; ++u) {
+            const int q = sg + SG * u;
+            if (act && q < P) {
+                const uint32_t pos = tileBase + (uint32_t)((q * Rec<N>::COLS + c) * 16 + r0);
+                ok = ok && t[u][1] == rec_tag(pos, epoch) && t[u][3] == rec_tag(pos + 1u, epoch);
+                acc.x = acc.x + __uint_as_float(t[u][0]);
+                acc.y = acc.y + __uint_as_float(t[u][2]);
+            }
+        }
+        return ok;
+    }
+};
+
 template <int N>
 __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int ntiles, int r, int R,
                                            bool local, float *lds)
 {
     using RC = Rec<N>;
-    constexpr int M = RC::M;
     constexpr int COLS = RC::COLS;
-    constexpr int ITEMS = COLS * 8;
-    constexpr int SG = (kWaves * 64) / ITEMS;
-    constexpr int U = 16;  // record loads in flight per thread
-    static_assert(SG >= 1 && SG * ITEMS <= kWaves * 64, "reducer layout");
-    float *sums = lds;                    // [SG][ITEMS][2]
-    float *irs = lds + SG * ITEMS * 2;    // [16] invRms per row
+    constexpr int kSg1 = (kWaves * 64) / ((N + 1) * 8);
+    constexpr int kSg2 = (kWaves * 64) / ((COLS - N - 1) * 8);
+    using Poll1 = ColPoll<N, 0, N + 1, (kMaxSlices + kSg1 - 1) / kSg1>;
+    using Poll2 = ColPoll<N, N + 1, COLS - N - 1, (kMaxSlices + kSg2 - 1) / kSg2>;
+    constexpr int kSums = Poll1::SG * Poll1::ITEMS > Poll2::SG * Poll2::ITEMS ? Poll1::SG * Poll1::ITEMS
+                                                                              : Poll2::SG * Poll2::ITEMS;
+    float *sums = lds;                // [SG][ITEMS][2] of the current phase
+    float *irs = lds + 2 * kSums;     // [16] invRms per row
     const int tid = threadIdx.x;
-    const int item = tid % ITEMS;
-    const int sg = tid / ITEMS;
-    const bool act = sg < SG;
-    const int c = item >> 3;
-    const int r0 = 2 * (item & 7);
     const int P = a.P;
     const uint32_t epoch = a.epoch;
     const float alphaPre = a.alpha[0];
     const float alphaPost = a.alpha[1];
     const float alphaRes = a.alpha[2];
+    Poll1 p1(tid);
+    Poll2 p2(tid);
+    // The bias of this thread's column in each phase, loaded once.
+    const float bias1 = a.bias[p1.c < N ? p1.c : 0];
+    const float bias2 = a.bias[p2.c - 1];
     bool timedOut = false;
     for (int k = r; k < ntiles; k += R) {
         const int rt = team + a.numTeams * k;
         const uint32_t slot = (uint32_t)(team * kRingSlots + k % kRingSlots);
-        const __amdgpu_buffer_rsrc_t tr =
-            make_rsrc(a.recs + (uint64_t)slot * P * RC::WORDS, P * RC::WORDS * 8);
+        const __amdgpu_buffer_rsrc_t tr = make_rsrc(a.recs + (uint64_t)slot * P * RC::WORDS, P * RC::WORDS * 8);
         const uint32_t tileBase = (uint32_t)(rt * P * RC::WORDS);
+
+        // Phase 1: hPre columns and sum of squares.
         float2 acc;
         for (uint32_t spins = 0;; ++spins) {
-            acc = make_float2(0.f, 0.f);
-            bool ok = true;
-            if (act) {
-                for (int q0 = sg; q0 < P; q0 += SG * U) {
-                    u32x4_t t[U];
-#pragma unroll
-                    for (int u = 0; u < U; ++u) {
-                        const int q = q0 + SG * u;
-                        t[u] = q < P ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                       tr, ((q * COLS + c) * 16 + r0) * 8, 0,
-                                                                       kCpolDev))
-                                     : u32x4_t{0u, 0u, 0u, 0u};
-                    }
-#pragma unroll
-                    for (int u = 0; u < U; ++u) {
-                        const int q = q0 + SG * u;
-                        if (q < P) {
-                            const uint32_t pos = tileBase + (uint32_t)((q * COLS + c) * 16 + r0);
-                            ok = ok && t[u][1] == rec_tag(pos, epoch) && t[u][3] == rec_tag(pos + 1u, epoch);
-                            acc.x = acc.x + __uint_as_float(t[u][0]);
-                            acc.y = acc.y + __uint_as_float(t[u][2]);
-                        }
-                    }
-                }
-            }
-            const bool all = __syncthreads_and(ok) != 0;
-            if (all || timedOut) {
+            p1.issue(tr, P);
+            const bool ok = p1.sum(tileBase, epoch, P, acc);
+            if (__syncthreads_and(ok) != 0 || timedOut) {
                 break;
             }
             if (spins >= a.spinLimit) {
@@ -293,73 +332,95 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
             }
             __builtin_amdgcn_s_sleep(2);
         }
-        if (act) {
-            sums[(sg * ITEMS + item) * 2] = acc.x;
-            sums[(sg * ITEMS + item) * 2 + 1] = acc.y;
+        p2.issue(tr, P);
+        if (p1.act) {
+            sums[(p1.sg * Poll1::ITEMS + tid % Poll1::ITEMS) * 2] = acc.x;
+            sums[(p1.sg * Poll1::ITEMS + tid % Poll1::ITEMS) * 2 + 1] = acc.y;
         }
         __syncthreads();
         float2 tot = make_float2(0.f, 0.f);
-        if (tid < ITEMS) {
+        if (tid < Poll1::ITEMS) {
 #pragma unroll
-            for (int g = 0; g < SG; ++g) {
-                tot.x = tot.x + sums[(g * ITEMS + item) * 2];
-                tot.y = tot.y + sums[(g * ITEMS + item) * 2 + 1];
+            for (int g = 0; g < Poll1::SG; ++g) {
+                tot.x = tot.x + sums[(g * Poll1::ITEMS + tid) * 2];
+                tot.y = tot.y + sums[(g * Poll1::ITEMS + tid) * 2 + 1];
             }
-            if (c == N) {  // sum of squares: invRms of rows r0, r0 + 1
-                irs[r0] = ref_inv_rms(tot.x, a.invFlatDim, a.normEps);
-                irs[r0 + 1] = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
+            if (p1.c == N) {  // sum of squares: invRms of rows r0, r0 + 1
+                irs[p1.r0] = ref_inv_rms(tot.x, a.invFlatDim, a.normEps);
+                irs[p1.r0 + 1] = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
             }
         }
         __syncthreads();
-        if (tid < ITEMS && c != N) {
-            const float ir0 = irs[r0];
-            const float ir1 = irs[r0 + 1];
-            if (c < N) {
-                // hPre column c: broadcast words (rows r0, r0 + 1) and the
-                // optional hPre output.
-                const float bc = a.bias[c];
-                u32x4_t wv;
+        if (tid < Poll1::ITEMS && p1.c < N) {
+            // hPre column c: broadcast words (rows r0, r0 + 1) and the
+            // optional hPre output.
+            const int c = p1.c;
+            u32x4_t wv;
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const float ir = e == 0 ? ir0 : ir1;
-                    const float mix = e == 0 ? tot.x : tot.y;
-                    const float v = ref_sigmoid(mix * (ir * alphaPre), bc, a.hcEps);
-                    const int idx = c * 16 + r0 + e;
-                    wv[2 * e] = __float_as_uint(v);
-                    wv[2 * e + 1] = bcast_tag((uint32_t)(rt * RC::BWORDS) + idx, epoch);
-                    const int row = rt * 16 + r0 + e;
-                    if (a.hPre != nullptr && row < a.T) {
-                        a.hPre[(int64_t)row * N + c] = v;
-                    }
+            for (int e = 0; e < 2; ++e) {
+                const float ir = irs[p1.r0 + e];
+                const float mix = e == 0 ? tot.x : tot.y;
+                const float v = ref_sigmoid(mix * (ir * alphaPre), bias1, a.hcEps);
+                const int idx = c * 16 + p1.r0 + e;
+                wv[2 * e] = __float_as_uint(v);
+                wv[2 * e + 1] = bcast_tag((uint32_t)(rt * RC::BWORDS) + idx, epoch);
+                const int row = rt * 16 + p1.r0 + e;
+                if (a.hPre != nullptr && row < a.T) {
+                    a.hPre[(int64_t)row * N + c] = v;
                 }
-                const __amdgpu_buffer_rsrc_t br =
-                    make_rsrc(a.bcast + (uint64_t)slot * RC::BWORDS, RC::BWORDS * 8);
-                if (local) {
-                    store16<0>(wv, br, (c * 16 + r0) * 8);
-                } else {
-                    store16<kCpolDev>(wv, br, (c * 16 + r0) * 8);
-                }
+            }
+            const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bcast + (uint64_t)slot * RC::BWORDS, RC::BWORDS * 8);
+            if (local) {
+                store16<0>(wv, br, (c * 16 + p1.r0) * 8);
             } else {
-                // Mix column j = c - 1 (N .. M-1): hPost or hRes.
-                const int jj = c - 1;
+                store16<kCpolDev>(wv, br, (c * 16 + p1.r0) * 8);
+            }
+        }
+
+        // Phase 2: hPost / hRes columns (loads issued above).
+        for (uint32_t spins = 0;; ++spins) {
+            const bool ok = p2.sum(tileBase, epoch, P, acc);
+            if (__syncthreads_and(ok) != 0 || timedOut) {
+                break;
+            }
+            if (spins >= a.spinLimit) {
+                record_timeout(a, tid);
+                timedOut = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            p2.issue(tr, P);
+        }
+        if (p2.act) {
+            sums[(p2.sg * Poll2::ITEMS + tid % Poll2::ITEMS) * 2] = acc.x;
+            sums[(p2.sg * Poll2::ITEMS + tid % Poll2::ITEMS) * 2 + 1] = acc.y;
+        }
+        __syncthreads();
+        if (tid < Poll2::ITEMS) {
+            tot = make_float2(0.f, 0.f);
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int row = rt * 16 + r0 + e;
-                    const float v = e == 0 ? tot.x : tot.y;
-                    const float ir = e == 0 ? ir0 : ir1;
-                    if (row < a.T) {
-                        if (jj < 2 * N) {
-                            const float sgm = ref_sigmoid(v * (ir * alphaPost), a.bias[jj], 0.0f);
-                            a.hPost[(int64_t)row * N + (jj - N)] = sgm * 2.0f;
-                        } else {
-                            const float rr = v * (ir * alphaRes);
-                            a.hRes[(int64_t)row * (N * N) + (jj - 2 * N)] = rr + a.bias[jj];
-                        }
+            for (int g = 0; g < Poll2::SG; ++g) {
+                tot.x = tot.x + sums[(g * Poll2::ITEMS + tid) * 2];
+                tot.y = tot.y + sums[(g * Poll2::ITEMS + tid) * 2 + 1];
+            }
+            // Mix column j = c - 1 (N .. M-1): hPost or hRes.
+            const int jj = p2.c - 1;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int row = rt * 16 + p2.r0 + e;
+                const float v = e == 0 ? tot.x : tot.y;
+                const float ir = irs[p2.r0 + e];
+                if (row < a.T) {
+                    if (jj < 2 * N) {
+                        const float sgm = ref_sigmoid(v * (ir * alphaPost), bias2, 0.0f);
+                        a.hPost[(int64_t)row * N + (jj - N)] = sgm * 2.0f;
+                    } else {
+                        const float rr = v * (ir * alphaRes);
+                        a.hRes[(int64_t)row * (N * N) + (jj - 2 * N)] = rr + bias2;
                     }
                 }
             }
         }
-        static_assert(M - N <= ITEMS, "columns");
         __syncthreads();  // sums / irs are reused by the next tile
     }
 }
@@ -501,30 +562,44 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     // holds, for lane l, B[k = s*D + col0 + 32q + 8(l/16) + e][slot 16ct +
     // l%16], e = 0..7, with ks = 2s + q.  The G waves of a strip share the
     // k-steps (wave of group g builds ks = g, g + G, ...).
+    //    All of a wave's phi and gamma loads are issued before the first
+    //    use, so the build costs one memory round trip.
     u32x4_t (*bfr)[NT][64] = bsh[strip];
-    for (int ks = half; ks < KS; ks += kGroups) {
-        const int s = ks >> 1;
-        const int q = ks & 1;
-        const int64_t k0 = (int64_t)s * a.D + col0 + 32 * q + 8 * grp;
-        f32x4_t gm0 = f32x4_t{1.f, 1.f, 1.f, 1.f}, gm1 = gm0;
-        if (a.gamma != nullptr) {
-            gm0 = *reinterpret_cast<const f32x4_t *>(a.gamma + k0);
-            gm1 = *reinterpret_cast<const f32x4_t *>(a.gamma + k0 + 4);
-        }
+    constexpr int KW = KS / kGroups;  // k-steps built per wave
+    const bool hasGamma = a.gamma != nullptr;
+    f32x4_t ph[KW][NT][2];
+    f32x4_t gm[KW][2];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) {
+        const int ks = half + kGroups * i;
+        const int64_t k0 = (int64_t)(ks >> 1) * a.D + col0 + 32 * (ks & 1) + 8 * grp;
 #pragma unroll
         for (int ct = 0; ct < NT; ++ct) {
             bool lo;
             int jc;
             CL::slot(16 * ct + rl, lo, jc);
             const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)jc * a.K + k0);
-            const f32x4_t ph0 = src[0];
-            const f32x4_t ph1 = src[1];
+            ph[i][ct][0] = src[0];
+            ph[i][ct][1] = src[1];
+        }
+        const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(hasGamma ? a.gamma + k0 : a.phi);
+        gm[i][0] = gsrc[0];
+        gm[i][1] = gsrc[1];
+    }
+#pragma unroll
+    for (int i = 0; i < KW; ++i) {
+        const int ks = half + kGroups * i;
+#pragma unroll
+        for (int ct = 0; ct < NT; ++ct) {
+            bool lo;
+            int jc;
+            CL::slot(16 * ct + rl, lo, jc);
             float out[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                float bv = e < 4 ? ph0[e] : ph1[e - 4];
-                if (a.gamma != nullptr) {
-                    bv = bv * (e < 4 ? gm0[e] : gm1[e - 4]);
+                float bv = ph[i][ct][e >> 2][e & 3];
+                if (hasGamma) {
+                    bv = bv * gm[i][e >> 2][e & 3];
                 }
                 const float hi = bf16_bits_to_f32(f32_to_bf16_bits(bv));
                 out[e] = lo ? (bv - hi) : hi;
@@ -849,6 +924,13 @@ hipError_t launch_strip(const Plan &p, void *workspace, uint32_t epoch, hipStrea
 }
 
 int strip_ring_slots() { return kRingSlots; }
+
+int strip_max_slices() { return kMaxSlices; }
+
+int strip_reducers(int available)
+{
+    return available >= 4 ? 4 : available >= 2 ? 2 : available;
+}
 
 int strip_max_coresident(const Plan &p, int numCUs)
 {
