@@ -204,6 +204,15 @@ __device__ __forceinline__ void record_timeout(const StripArgs &a, int lane)
     }
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also makes every
+// outstanding global load and store of the wave complete first.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // A fragments of k-steps 2q and 2q + 1 from the line-layout registers r0
 // (rows 0-7) and r1 (rows 8-15): lanes with bit 3 set take the other
 // register's lane l ^ 8 (DPP row_ror:8 with banks 2-3 or 0-1 enabled).
@@ -233,11 +242,10 @@ __device__ __forceinline__ f32x4_t mfma16_f16(const u32x4_t &a, const u32x4_t &b
 //   carry its tag; the whole workgroup retries until all do.  The groups are
 //   then added in order in LDS, invRms and hPre are evaluated, and hPre is
 //   published (the broadcast block).
-//   Phase 2 reads the hPost / hRes columns N+1 .. M the same way (their
-//   loads go out before the hPre arithmetic) and writes those outputs.
-// Every sum has a fixed order.  hPre is published only after every column of
-// every record of the tile has been read by the phase-2 loads issued before
-// it, so a slice that has seen the block may reuse the tile's ring slot.
+//   Phase 2 then reads the hPost / hRes columns N+1 .. M the same way and
+//   writes those outputs.
+// Every sum has a fixed order.  The ring size (kRingSlots) keeps a slot from
+// being rewritten before its reducer has finished both phases.
 template <int N, int C0, int NC, int UMAX>
 struct ColPoll {
     static constexpr int ITEMS = NC * 8;
@@ -332,12 +340,11 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
             }
             __builtin_amdgcn_s_sleep(2);
         }
-        p2.issue(tr, P);
         if (p1.act) {
             sums[(p1.sg * Poll1::ITEMS + tid % Poll1::ITEMS) * 2] = acc.x;
             sums[(p1.sg * Poll1::ITEMS + tid % Poll1::ITEMS) * 2 + 1] = acc.y;
         }
-        __syncthreads();
+        lds_barrier();
         float2 tot = make_float2(0.f, 0.f);
         if (tid < Poll1::ITEMS) {
 #pragma unroll
@@ -350,7 +357,7 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
                 irs[p1.r0 + 1] = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (tid < Poll1::ITEMS && p1.c < N) {
             // hPre column c: broadcast words (rows r0, r0 + 1) and the
             // optional hPre output.
@@ -377,8 +384,9 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
             }
         }
 
-        // Phase 2: hPost / hRes columns (loads issued above).
+        // Phase 2: hPost / hRes columns.
         for (uint32_t spins = 0;; ++spins) {
+            p2.issue(tr, P);
             const bool ok = p2.sum(tileBase, epoch, P, acc);
             if (__syncthreads_and(ok) != 0 || timedOut) {
                 break;
@@ -389,13 +397,12 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
-            p2.issue(tr, P);
         }
         if (p2.act) {
             sums[(p2.sg * Poll2::ITEMS + tid % Poll2::ITEMS) * 2] = acc.x;
             sums[(p2.sg * Poll2::ITEMS + tid % Poll2::ITEMS) * 2 + 1] = acc.y;
         }
-        __syncthreads();
+        lds_barrier();
         if (tid < Poll2::ITEMS) {
             tot = make_float2(0.f, 0.f);
 #pragma unroll
@@ -421,7 +428,7 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
                 }
             }
         }
-        __syncthreads();  // sums / irs are reused by the next tile
+        lds_barrier();  // sums / irs are reused by the next tile
     }
 }
 
@@ -438,8 +445,12 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     constexpr int E = kLag;
     constexpr int KS = 2 * N;  // 32-column k-steps per strip (two per stream)
     static_assert(N == 4, "the strip path is built for n = 4");
-    // Partials of the four strips of each group, double-buffered by own step.
-    __shared__ __attribute__((aligned(16))) float part[kGroups][2][kStrips][RC::COLS * 16];
+    // Partials of the four strips of each group, double-buffered by own step:
+    // column c of a strip's partial at c * kColPitch floats.  The pitch (20,
+    // not 16) puts the 16-byte writes of 8 consecutive lanes (consecutive
+    // columns) on distinct LDS banks.
+    constexpr int kColPitch = 20;
+    __shared__ __attribute__((aligned(16))) float part[kGroups][2][kStrips][RC::COLS * kColPitch];
     // B operand of each strip, in MFMA fragment order (24 KB per strip).
     __shared__ u32x4_t bsh[kStrips][KS][NT][64];
     // Per-group count of partials written (4 per own step).
@@ -542,28 +553,13 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             xb[b][s][1] = u32x4_t{0u, 0u, 0u, 0u};
         }
     }
-    // The ring: slot jj mod L holds own tile jj.  Tiles 0 .. L-E-1 are loaded
-    // here; step jj loads tile jj - E + L.
-#pragma unroll
-    for (int b = 0; b < L - E; ++b) {
-        const __amdgpu_buffer_rsrc_t r = make_rsrc(x_tile(b), rows_of(b) * Ki * 2);
-#pragma unroll
-        for (int s = 0; s < N; ++s) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                xb[b][s][h] = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, xLane + (8 * h * Ki + s * Di) * 2,
-                                                                   0, kCpolNt));
-            }
-        }
-    }
-
     // B operand of each strip, in LDS for the whole launch: fragment (ks, ct)
     // holds, for lane l, B[k = s*D + col0 + 32q + 8(l/16) + e][slot 16ct +
     // l%16], e = 0..7, with ks = 2s + q.  The G waves of a strip share the
     // k-steps (wave of group g builds ks = g, g + G, ...).
     //    All of a wave's phi and gamma loads are issued before the first
-    //    use, so the build costs one memory round trip.
+    //    use, so the build costs one memory round trip; the first x tiles
+    //    are loaded behind them.
     u32x4_t (*bfr)[NT][64] = bsh[strip];
     constexpr int KW = KS / kGroups;  // k-steps built per wave
     const bool hasGamma = a.gamma != nullptr;
@@ -586,6 +582,24 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         gm[i][0] = gsrc[0];
         gm[i][1] = gsrc[1];
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // The ring: slot jj mod L holds own tile jj.  Tiles 0 .. L-E-1 are loaded
+    // here, after the phi and gamma loads (which the B build then waits for
+    // without waiting for these); step jj loads tile jj - E + L.
+#pragma unroll
+    for (int b = 0; b < L - E; ++b) {
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(x_tile(b), rows_of(b) * Ki * 2);
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                xb[b][s][h] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, xLane + (8 * h * Ki + s * Di) * 2,
+                                                                   0, kCpolNt));
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < KW; ++i) {
         const int ks = half + kGroups * i;
@@ -607,7 +621,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             bfr[ks][ct][lane] = pack8_bf16(out);
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // Every step issues the same memory operations in the same order (two
     // hIn stores, one broadcast poll, eight x loads, one record store per
@@ -627,6 +641,11 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     // Exchange ring slot of own step jj (team step G jj + group).
     auto slot_of = [&](int jj) { return teamI * kRingSlots + (kGroups * jj + half) % kRingSlots; };
     bool timedOut = false;
+
+    // Meeting count of the other group once it has run all its steps (each
+    // group runs whole rounds of L steps).
+    const int nmineOther = (nt32 - (half ^ 1) + kGroups - 1) / kGroups;
+    const uint32_t otherCount = 4u * (uint32_t)(((nmineOther + E + L - 1) / L) * L);
 
     for (int j0 = 0; j0 < nmine + E; j0 += L) {
 #pragma unroll
@@ -792,7 +811,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
 #pragma unroll
             for (int t = 0; t < Q; ++t) {
                 const f32x4_t v = acc[t] + acc[Q + t];
-                *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * t + rl) * 16 + 4 * grp) = v;
+                *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * t + rl) * kColPitch + 4 * grp) = v;
             }
             if constexpr (CL::kHalfTile) {
                 f32x4_t o;
@@ -801,26 +820,33 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                     o[i] = __shfl_xor(acc[2 * Q][i], 8);
                 }
                 if (rl < 8) {
-                    *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * Q + rl) * 16 + 4 * grp) =
+                    *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * Q + rl) * kColPitch + 4 * grp) =
                         acc[2 * Q] + o;
                 }
             }
             if ((rl >> 2) == grp) {
-                mine[N * 16 + rl] = ss;
+                mine[N * kColPitch + rl] = ss;
             }
-            //    The four strips of this half meet through an LDS counter
-            //    (the other half keeps running): each adds one after its
+            //    The four strips of this group meet through an LDS counter
+            //    (the other group keeps running): each adds one after its
             //    partials, then waits for 4 (jj + 1).  A strip writes this
             //    buffer again two steps later, after the next meeting, by
-            //    which time every strip has read it.
+            //    which time every strip has read it.  The wait also holds a
+            //    group that is a step ahead of the other (count below 4 jj):
+            //    the SIMDs favour the older waves, and a group left to run
+            //    ahead finishes early and leaves the other to run the last
+            //    steps alone.  The wait for the other group is capped at
+            //    its final count, so it always ends.
             {
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
                 if (lane == 0) {  // one count per wave
                     __hip_atomic_fetch_add(&arrived[half], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
                 const uint32_t target = 4u * (uint32_t)(jj + 1);
-                while (__hip_atomic_load(&arrived[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
-                       target) {
+                const uint32_t otherTarget = min(target - 4u, otherCount);
+                while (__hip_atomic_load(&arrived[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target ||
+                       __hip_atomic_load(&arrived[half ^ 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                           otherTarget) {
                     __builtin_amdgcn_s_sleep(1);
                 }
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
@@ -836,10 +862,11 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 const int c = ch >> 3;
                 const int r0 = 2 * (ch & 7);
                 const float *pb = &part[half][jj & 1][0][0];
-                float2 v = *reinterpret_cast<const float2 *>(pb + c * 16 + r0);
+                float2 v = *reinterpret_cast<const float2 *>(pb + c * kColPitch + r0);
 #pragma unroll
                 for (int st = 1; st < kStrips; ++st) {
-                    const float2 u = *reinterpret_cast<const float2 *>(pb + st * RC::COLS * 16 + c * 16 + r0);
+                    const float2 u =
+                        *reinterpret_cast<const float2 *>(pb + st * RC::COLS * kColPitch + c * kColPitch + r0);
                     v.x = v.x + u.x;
                     v.y = v.y + u.y;
                 }
