@@ -119,8 +119,11 @@ def measured_traffic(workload: str, path: str):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # Defaults: the device's clocks settle within about 20 ms of sustained load
+    # (launches 20-50 of a cold start run up to 30% slower than the steady
+    # state), so 300 warm-up launches (~35 ms) precede 1000 timed ones (~0.12 s).
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--config", type=int, default=3, choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target duration of the CPU-baseline sample (0 disables it)")
