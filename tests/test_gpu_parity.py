@@ -195,6 +195,32 @@ def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_ga
     check(out, ref, x, is_bf16, orc)
 
 
+@pytest.mark.parametrize("T,D,is_bf16,has_gamma", [
+    (6144 + 5, 1536, True, True),    # P = 6: 4 teams per XCD, 2 reducers each; 12+ steps per team
+    (4096, 3584, False, True),       # P = 14: 2 teams per XCD, 2 reducers each
+    (3072 - 3, 7936, True, False),   # P = 31, the largest team: 1 reducer; 24 steps per team
+    (40, 7168, True, True),          # 3 row tiles for 8 teams: most teams have no tile
+])
+def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
+    """Team geometries of the strip kernel on a 32-CU-per-XCD device: reducer
+    counts 1 and 2 (the exchange ring's size argument covers R = 1, 2, 4),
+    the largest slice count, enough tiles per team to wrap the ring of 10
+    slots several times, and teams without tiles."""
+    n = 4
+    rng = np.random.default_rng(T * 7 + D)
+    K, M = n * D, n * n + 2 * n
+    x = to_bits(rng.standard_normal((T, n, D)).astype(np.float32), is_bf16)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.asarray([0.3, -0.2, 0.05], dtype=np.float32)
+    bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
+    _say(f"[strip-teams] T={T} D={D} bf16={is_bf16} gamma={has_gamma}")
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
+    assert out["path"] == "strip"
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
+    check(out, ref, x, is_bf16, orc)
+
+
 def test_attributes_and_hpre_off(pkg, orc, device):
     """Non-default normEps/hcEps (hcEps = 0 skips the add, mhc_pre.cpp:552) and the
     3-output entry point (no hPre)."""
