@@ -24,3 +24,10 @@ from .binding import (  # noqa: F401
     make_tensor,
     mhc_pre,
 )
+
+
+def torch_ops():
+    """Register and return the ``torch.ops.mhcpre`` operators (module torch_op)."""
+    from . import torch_op
+
+    return torch_op
