@@ -382,6 +382,10 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
     bool done = false;
     int device = -1;
     DeviceShape shape;
+    // The launches' status is read back with hipGetLastError: first clear an
+    // error an earlier call of the process may have left there (the split
+    // path makes no other HIP call before its first launch).
+    (void)hipGetLastError();
     if (p.path != mhc::Path::kSplit && !device_shape(device, shape)) {
         return MHC_STATUS_HIP_ERROR;
     }

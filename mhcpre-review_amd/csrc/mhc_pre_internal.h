@@ -11,7 +11,7 @@ namespace mhc {
 enum class Path : int {
     kSplit = 0,   // prep B, split-K MFMA GEMM + sumsq partials, epilogue + hIn (x read twice)
     kFused = 1,   // one persistent kernel: x read once, kept in registers
-    kStrip = 2,   // one persistent kernel: XCD-local teams, B in registers, x in a register ring
+    kStrip = 2,   // one persistent kernel: XCD-local teams, B in LDS, x in a register ring
 };
 
 // Device status word (first 8 bytes of the workspace): the low half holds a
