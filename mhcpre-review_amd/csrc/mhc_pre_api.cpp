@@ -263,13 +263,49 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     if (n == 4 && (D % 256) == 0 && D / 256 <= mhc::strip_max_slices() && T < (int64_t{1} << 24)) {
         p.stripP = static_cast<int>(D / 256);
     }
+    // Rows path (n = 6, 8): 256-row blocks x K-ranges of whole 4-k-step
+    // stages.  The K-range count balances whole waves of 256 workgroups (one
+    // per CU of an MI355X; the count only affects speed) against the partial
+    // traffic: cost ~ rounds * (x bytes of one item) + partial bytes written
+    // and read.  32-bit buffer offsets bound K and the B bytes of a range.
+    if ((n == 6 || n == 8) && (K % 128) == 0 && K < (int64_t{1} << 25)) {
+        const int64_t blockRows = mhc::rows_block_rows();
+        const int64_t stageKs = mhc::rows_stage_ksteps();
+        const int64_t blocks = (T + blockRows - 1) / blockRows;
+        const int64_t KS = K / 32;
+        constexpr int64_t kSlotsPerRound = 256;
+        double best = -1.0;
+        for (int64_t s = 1; s <= KS / stageKs; ++s) {
+            const int64_t ksPer = stageKs * ((KS + stageKs * s - 1) / (stageKs * s));
+            const int64_t S = (KS + ksPer - 1) / ksPer;
+            if (S != s) {
+                continue;
+            }
+            const int64_t rounds = (blocks * S + kSlotsPerRound - 1) / kSlotsPerRound;
+            const double cost = static_cast<double>(rounds) * static_cast<double>(std::min(T, blockRows)) *
+                                    static_cast<double>(ksPer) * 64.0 * kSlotsPerRound +
+                                2.0 * static_cast<double>(S) * static_cast<double>(T) * (M + 1) * 4.0;
+            if (best < 0.0 || cost < best) {
+                best = cost;
+                p.rowsS = static_cast<int>(S);
+                p.rowsKsPer = static_cast<int>(ksPer);
+            }
+        }
+        if (static_cast<int64_t>(p.rowsKsPer) * p.NT * 1024 >= (int64_t{1} << 31)) {
+            p.rowsS = 0;
+        }
+        p.rowsBlocks = static_cast<int>(blocks);
+    }
     p.path = p.stripP > 0 ? mhc::Path::kStrip
-                          : (p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit);
+                          : (p.fusedP > 0 ? mhc::Path::kFused
+                                          : (p.rowsS > 0 ? mhc::Path::kRows : mhc::Path::kSplit));
     if (const char *force = std::getenv("MHCPRE_FORCE_PATH")) {
         if (std::strcmp(force, "split") == 0) {
             p.path = mhc::Path::kSplit;
         } else if (std::strcmp(force, "fused") == 0 && p.fusedP > 0) {
             p.path = mhc::Path::kFused;
+        } else if (std::strcmp(force, "rows") == 0 && p.rowsS > 0) {
+            p.path = mhc::Path::kRows;
         }
     }
     if (const char *launch = std::getenv("MHCPRE_LAUNCH")) {
@@ -306,7 +342,16 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         fusedEnd = align_up(
             p.wsFusedPartial + recSlots * p.fusedP * mhc::fused_record_words(n) * 8, 256);
     }
-    p.wsTotal = std::max(splitEnd, fusedEnd);
+    size_t rowsEnd = 0;
+    if (p.rowsS > 0) {
+        p.wsRowsB = mhc::kWsHeaderBytes;
+        p.wsRowsPartial =
+            align_up(p.wsRowsB + static_cast<size_t>(K / 32) * static_cast<size_t>(p.NT) * 1024, 256);
+        rowsEnd = align_up(p.wsRowsPartial + static_cast<size_t>(p.rowsS) * static_cast<size_t>(T) *
+                                                 static_cast<size_t>(M + 1) * 4,
+                           256);
+    }
+    p.wsTotal = std::max(std::max(splitEnd, fusedEnd), rowsEnd);
     return MHC_STATUS_SUCCESS;
 }
 
@@ -426,6 +471,11 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
             done = true;
         }
     }
+    if (!done && p.path == mhc::Path::kRows) {
+        executor->lastEpoch.store(next_epoch(), std::memory_order_relaxed);
+        err = mhc::launch_rows(p, workspace, shape.xcds, stream);
+        done = true;
+    }
     if (!done) {
         executor->lastEpoch.store(next_epoch(), std::memory_order_relaxed);
         err = mhc::launch_split(p, workspace, stream);
@@ -504,6 +554,9 @@ int mhcPreExecutorPath(const mhcPreExecutor *executor, const char **name)
         break;
     case mhc::Path::kFused:
         *name = "fused";
+        break;
+    case mhc::Path::kRows:
+        *name = "rows";
         break;
     default:
         *name = "split";

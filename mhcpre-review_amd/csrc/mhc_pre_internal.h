@@ -12,6 +12,7 @@ enum class Path : int {
     kSplit = 0,   // prep B, split-K MFMA GEMM + sumsq partials, epilogue + hIn (x read twice)
     kFused = 1,   // one persistent kernel: x read once, kept in registers
     kStrip = 2,   // one persistent kernel: XCD-local teams, B in LDS, x in a register ring
+    kRows = 3,    // prep B, split-K GEMM over 256-row blocks (B through an LDS ring), epilogue + hIn
 };
 
 // Device status word (first 8 bytes of the workspace): the low half holds a
@@ -72,12 +73,20 @@ struct Plan {
     int stripTeamsPerXcd = 0;
     int stripGrid = 0;
 
-    // Workspace layout (byte offsets).  The two paths' regions overlap: a
+    // Rows path (n = 6, 8; K % 128 == 0): rowsS K-ranges of rowsKsPer
+    // k-steps over rowsBlocks blocks of 256 rows.
+    int rowsS = 0;
+    int rowsKsPer = 0;
+    int rowsBlocks = 0;
+
+    // Workspace layout (byte offsets).  The paths' regions overlap: a
     // workspace holds one launch at a time.
     size_t wsBsplit = 0;      // split: B fragments
     size_t wsPartial = 0;     // split: [S][T][M+1] partials
     size_t wsFinal = 0;       // fused: per-tile hPre / invRms blocks (tagged words)
     size_t wsFusedPartial = 0;// fused: per-(tile, slice) exchange records (tagged words)
+    size_t wsRowsB = 0;       // rows: B fragments [K/32][NT][64 lanes] x 16 bytes
+    size_t wsRowsPartial = 0; // rows: [rowsS][T][M+1] partials
     size_t wsTotal = 0;
 
     // Bound device pointers (caller memory).
@@ -99,6 +108,13 @@ hipError_t launch_split(const Plan &plan, void *workspace, hipStream_t stream);
 hipError_t launch_fused(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
 
 hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
+
+// Rows path (mhc_pre_rows.hip); nXcd: XCDs of the device (work-item placement
+// only).
+hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, hipStream_t stream);
+// Rows per work item and k-steps per stage of the rows-path GEMM.
+int rows_block_rows();
+int rows_stage_ksteps();
 
 // Workgroups of the strip kernel that can be resident per CU (x numCUs), or
 // -1 if the plan has no strip kernel.

@@ -1,0 +1,658 @@
+// Row-block kernels for gfx950 (rows path: n = 6 and n = 8, K % 128 == 0).
+//
+// Why x is read twice here.  For n = 8 the B operand of the mixing GEMM
+// (gamma * phi split into bf16 hi + lo, 2M = 160 columns) takes 320 bytes per
+// element of K.  A slice of K whose B fits one CU's LDS is at most ~450
+// elements wide, and the partial sums such a slice would have to hand to the
+// other slices of a row (M + 1 = 81 floats) are then as large as its share of
+// the row's x.  Keeping x on chip until hPre is known (as the persistent n = 4
+// kernels do) would move more bytes between CUs than it saves; so this path
+// runs a split-K GEMM that reads x once, and a second pass that reads x again
+// for hIn.  Three launches:
+//
+//   rows_prep_b    B fragments in the order the MFMA reads them:
+//                  [K/32 k-steps][NT tiles][64 lanes] x 16 bytes.  Tile t < Q
+//                  holds hi of columns 16t + l%16 and tile Q + t their lo, in
+//                  the same lanes; when M % 16 == 8 the last tile holds hi
+//                  (lanes 0-7 of each 16) and lo (lanes 8-15) of the last 8
+//                  columns.  Lane l holds k = 32ks + 8(l/16) .. +8.
+//   rows_gemm      split-K GEMM over work items (256-row block, K-range).  A
+//                  workgroup is 8 waves of 32 rows (two 16-row MFMA blocks).
+//                  K-ranges are walked in stages of 4 k-steps: each stage's B
+//                  fragments go into an LDS ring by direct-to-LDS buffer loads
+//                  (each wave copies NT/2 of its 4*NT fragments), its x into a
+//                  register ring as whole 128-byte lines (8 lanes per row), both
+//                  kAhead stages ahead of the MFMAs.  A DPP row_ror:8 turns two
+//                  line registers into the A fragments of two k-steps.  hi and
+//                  lo products accumulate into one fp32 accumulator per mix
+//                  column; a Gram MFMA of the same fragments gives the sum of
+//                  squares on its diagonal.  Writes partial[K-range][row][M+1]
+//                  (mix columns, then the sum of squares).
+//   rows_epilogue  one workgroup per row: the K-range partials summed in
+//                  K-range order, invRms, the sigmoid / affine epilogue
+//                  (code/op_kernel/mhc_pre.cpp:735-758), and hIn from a second
+//                  read of x with round-half-even stores
+//                  (code/op_kernel/mhc_pre.cpp:761-826).
+//
+// Work items map to XCDs so that the workgroups of one XCD share K-ranges:
+// workgroup g runs on XCD g mod X (round-robin dispatch) and takes item
+// (g mod X) * C + g / X of the X*C item slots, items numbered row block
+// fastest.  The B fragments of an item's K-range are then read by the other
+// row blocks of the same K-range from that XCD's L2.  The mapping affects
+// speed only.
+
+#include "mhc_pre_device.h"
+#include "mhc_pre_internal.h"
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mhc {
+namespace {
+
+using namespace dev;
+
+constexpr int kRW = 8;                       // waves per GEMM workgroup
+constexpr int kRowsWave = 32;                // rows per wave (two 16-row MFMA blocks)
+constexpr int kRowBlock = kRW * kRowsWave;   // rows per work item
+constexpr int kStageKs = 4;                  // k-steps per stage: two 128-byte lines of a row
+constexpr int kAhead = 2;                    // stages loading ahead of the MFMAs
+constexpr int kSlots = kAhead + 1;           // ring depth (x registers and B in LDS)
+constexpr int kEpiThreads = 512;             // epilogue workgroup
+constexpr int kEpiOct = 2;                   // hIn column octets per thread per pass
+
+// Column tiles of the B operand and the accumulator tile each one adds into.
+template <int N>
+struct RowsCols {
+    static constexpr int M = N * N + 2 * N;
+    static constexpr int Q = M / 16;
+    static constexpr bool kHalf = (M % 16) == 8;
+    static constexpr int NT = 2 * Q + (kHalf ? 1 : 0);  // = 2M / 16
+    static constexpr int NA = Q + (kHalf ? 1 : 0);      // accumulator tiles
+    static_assert(M % 16 == 0 || M % 16 == 8, "M = n*n + 2n is 24, 48 or 80");
+    static constexpr int acc(int t) { return t < Q ? t : (t < 2 * Q ? t - Q : Q); }
+    static constexpr bool hi_tile(int t) { return t < Q || t == 2 * Q; }
+};
+
+constexpr int kCpolNt = 2;  // nontemporal: hIn is written once
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, 0x00020000);
+}
+
+template <int kCpol>
+__device__ __forceinline__ u32x4_t load16(__amdgpu_buffer_rsrc_t r, int off)
+{
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpol));
+}
+
+// Waits until at most `kOut` of this wave's vector-memory loads are still in
+// flight (they complete in issue order), without waiting on LDS or exports.
+template <int kOut>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(kOut >= 0 && kOut < 64, "vmcnt range");
+    // s_waitcnt fields: vmcnt [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+    constexpr int imm = (kOut & 15) | ((kOut >> 4) << 14) | (7 << 4) | (15 << 8);
+    __builtin_amdgcn_s_waitcnt(imm);
+}
+
+// Workgroup barrier that orders LDS only (no wait for outstanding global
+// loads, which __syncthreads() would add).
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// A fragments of k-steps 2q and 2q + 1 from line-layout registers r0 (rows
+// 0-7) and r1 (rows 8-15).  In a line register lane l holds row l & 7 and the
+// 8 columns at 8(l >> 4) + 32((l >> 3) & 1) of a 64-column line; the A
+// fragment wants row l & 15 and columns 8(l >> 4) of its k-step, so lanes
+// with bit 3 set take the other register's lane l ^ 8 (DPP row_ror:8 with
+// banks 2-3 or 0-1 enabled).
+__device__ __forceinline__ void lines_to_frags(const u32x4_t &r0, const u32x4_t &r1, u32x4_t &k0,
+                                               u32x4_t &k1)
+{
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        k0[w] = (uint32_t)__builtin_amdgcn_update_dpp((int)r0[w], (int)r1[w], 0x128, 0xF, 0xC, false);
+        k1[w] = (uint32_t)__builtin_amdgcn_update_dpp((int)r1[w], (int)r0[w], 0x128, 0xF, 0x3, false);
+    }
+}
+
+__device__ __forceinline__ f32x4_t mfma16_f16(const u32x4_t &a, const u32x4_t &b, const f32x4_t &c)
+{
+    typedef _Float16 f16x8_t __attribute__((__vector_size__(8 * sizeof(_Float16))));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// rows_prep_b: one thread per (k-step, accumulator tile, lane): reads 8 k of
+// one phi column (and gamma), writes the hi and the lo fragment lanes.
+// ---------------------------------------------------------------------------
+template <int N>
+__global__ __launch_bounds__(256) void rows_prep_b_kernel(const float *__restrict__ phi,
+                                                          const float *__restrict__ gamma,
+                                                          u32x4_t *__restrict__ bfrag, int64_t K,
+                                                          uint32_t *__restrict__ status)
+{
+    using C = RowsCols<N>;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx == 0 && status != nullptr) {
+        *status = kDeviceOk;
+    }
+    const int64_t total = (K / 32) * C::NA * kWave;
+    if (idx >= total) {
+        return;
+    }
+    const int lane = (int)(idx % kWave);
+    const int ta = (int)((idx / kWave) % C::NA);
+    const int64_t ks = idx / ((int64_t)kWave * C::NA);
+    int j, thi, tlo, lhi, llo;
+    if (ta < C::Q) {
+        j = 16 * ta + (lane & 15);
+        thi = ta;
+        tlo = C::Q + ta;
+        lhi = llo = lane;
+    } else {
+        if ((lane & 15) >= 8) {
+            return;
+        }
+        j = 16 * C::Q + (lane & 7);
+        thi = tlo = 2 * C::Q;
+        lhi = lane;
+        llo = lane + 8;
+    }
+    const int64_t k0 = ks * 32 + 8 * (lane >> 4);
+    const f32x4_t *src = reinterpret_cast<const f32x4_t *>(phi + (int64_t)j * K + k0);
+    const f32x4_t p0 = src[0], p1 = src[1];
+    float b[8] = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+    if (gamma != nullptr) {
+        const f32x4_t *gs = reinterpret_cast<const f32x4_t *>(gamma + k0);
+        const f32x4_t g0 = gs[0], g1 = gs[1];
+        const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            b[e] = b[e] * g[e];
+        }
+    }
+    float hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        hi[e] = bf16_bits_to_f32(f32_to_bf16_bits(b[e]));
+        lo[e] = b[e] - hi[e];
+    }
+    u32x4_t *dst = bfrag + ks * C::NT * kWave;
+    dst[thi * kWave + lhi] = pack8_bf16(hi);
+    dst[tlo * kWave + llo] = pack8_bf16(lo);
+}
+
+// ---------------------------------------------------------------------------
+// rows_gemm
+// ---------------------------------------------------------------------------
+struct RowsGemmArgs {
+    const uint16_t *x;
+    const u32x4_t *bfrag;
+    float *partial;  // [S][T][M + 1]
+    int64_t T;
+    int64_t K;
+    int ksPer;       // k-steps per K-range (a multiple of kStageKs)
+    int S;           // K-ranges
+    int rowBlocks;   // 256-row blocks
+    int perXcd;      // item slots per XCD
+    int nXcd;
+};
+
+template <int N, bool kBf16>
+__global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
+{
+    using C = RowsCols<N>;
+    constexpr int M = C::M;
+    constexpr int NT = C::NT;
+    constexpr int NA = C::NA;
+    constexpr int Q = C::Q;
+    constexpr int SF = kStageKs * NT;  // B fragments per stage
+    constexpr int NB = SF / kRW;       // of which each wave copies NB
+    static_assert(SF % kRW == 0, "each wave copies the same number of B fragments");
+    constexpr int kXLoads = 8;         // x line loads per wave and stage
+    constexpr int kUnroll = kSlots;    // steps per loop trip (static ring slots)
+    __shared__ u32x4_t bsh[kSlots][SF][kWave];
+
+    const int lane = threadIdx.x & 63;
+    // Wave-uniform (scalar) wave index: the buffer resources built from it
+    // stay in scalar registers.
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = blockIdx.x;
+    const int f = (g % a.nXcd) * a.perXcd + g / a.nXcd;
+    if (f >= a.rowBlocks * a.S) {
+        return;
+    }
+    const int rb = f % a.rowBlocks;
+    const int kr = f / a.rowBlocks;
+    const int KS = (int)(a.K / 32);
+    const int ks0 = kr * a.ksPer;
+    const int nst = min(a.ksPer, KS - ks0) / kStageKs;
+
+    // x of this wave's 32 rows, through a resource that covers the valid
+    // rows only: loads of rows past T return zeros.
+    const int64_t r0 = (int64_t)rb * kRowBlock + (int64_t)kRowsWave * w;
+    const int vrows = (int)max((int64_t)0, min((int64_t)kRowsWave, a.T - r0));
+    const int K2 = (int)(a.K * 2);  // row stride in bytes
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + (vrows > 0 ? r0 * a.K : 0), vrows * K2);
+    const int xLane = (lane & 7) * K2 + 2 * (8 * (lane >> 4) + 32 * ((lane >> 3) & 1)) + ks0 * 64;
+    // B fragments of this K-range.
+    const __amdgpu_buffer_rsrc_t br =
+        make_rsrc(a.bfrag + (int64_t)ks0 * NT * kWave, nst * SF * kWave * 16);
+
+    u32x4_t xs[kSlots][4][2];  // [slot][8-row group][line of the stage]
+    u32x4_t bst[NB];           // B fragments of a stage on their way to LDS
+
+    // Per-lane offsets are loop-invariant registers and the stage's part of
+    // each address is a scalar offset.
+    const int bLane = w * (kWave * 16) + lane * 16;
+    int xOff[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        xOff[h] = xLane + 8 * h * K2;
+    }
+
+    // Stage s's loads: its B fragments into the staging registers (they go
+    // to LDS one step later, just before the next stage's B reuses the
+    // registers), then its x lines into ring slot s mod kSlots.
+    // Every stage issues the same loads in the same order, live or not:
+    // stages past the K-range read through size-0 resources, so the counter
+    // waits below stay exact.
+    auto issue = [&](int s, u32x4_t(&bd)[NB], u32x4_t(&xd)[4][2]) {
+        const bool live = s < nst;
+        const __amdgpu_buffer_rsrc_t bq = live ? br : make_rsrc(a.bfrag, 0);
+        const __amdgpu_buffer_rsrc_t xq = live ? xr : make_rsrc(a.x, 0);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            bd[i] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(bq, bLane, (s * SF + kRW * i) * (kWave * 16), 0));
+        }
+        // Keep the B loads ahead of the x lines: waiting for them next step
+        // must not wait for this stage's x.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                xd[h][c] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xq, xOff[h] + 128 * c,
+                                                                   s * (kStageKs * 64), 0));
+            }
+        }
+    };
+    auto stash = [&](int sl, const u32x4_t(&bd)[NB]) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            bsh[sl][w + kRW * i][lane] = bd[i];
+        }
+    };
+
+    f32x4_t acc[2][NA];
+    f32x4_t gram[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        gram[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < NA; ++t) {
+            acc[r][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    // Prologue: stages 0 and 1 in flight, stage 0's B in LDS.
+    static_assert(kAhead == 2 && kSlots == 3, "ring geometry");
+    issue(0, bst, xs[0]);
+    wait_vm<kXLoads>();
+    stash(0, bst);
+    issue(1, bst, xs[1]);
+
+    // Step s: x of stage s and B of stage s + 1 have arrived once only the
+    // x lines of stage s + 1 may still be in flight.  The barrier makes every
+    // wave's stash of B(s) visible and tells every wave that all reads of
+    // slot (s + 1) mod 3 (last read at step s - 2) are done; B(s + 1) goes
+    // there, and stage s + 2's loads go out behind it.
+    // The trip count is rounded up to whole trips: the stages past the
+    // K-range read zeros for both x and B, and add nothing.
+    const int nstTrips = (nst + kUnroll - 1) / kUnroll * kUnroll;
+    for (int s0 = 0; s0 < nstTrips; s0 += kUnroll) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int s = s0 + u;
+            const int sl = u % kSlots;
+            wait_vm<kXLoads>();
+            lds_barrier();
+            stash((u + 1) % kSlots, bst);
+            issue(s + 2, bst, xs[(u + 2) % kSlots]);
+            if (vrows > 0) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    u32x4_t af[2][2];  // [16-row block][k-step of the line]
+                    lines_to_frags(xs[sl][0][c], xs[sl][1][c], af[0][0], af[0][1]);
+                    lines_to_frags(xs[sl][2][c], xs[sl][3][c], af[1][0], af[1][1]);
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk) {
+                        const int ksl = 2 * c + kk;
+                        if constexpr (kBf16) {
+#pragma unroll
+                            for (int t = 0; t < NT; ++t) {
+                                const u32x4_t b = bsh[sl][ksl * NT + t][lane];
+                                acc[0][C::acc(t)] = mfma16(af[0][kk], b, acc[0][C::acc(t)]);
+                                acc[1][C::acc(t)] = mfma16(af[1][kk], b, acc[1][C::acc(t)]);
+                            }
+                            gram[0] = mfma16(af[0][kk], af[0][kk], gram[0]);
+                            gram[1] = mfma16(af[1][kk], af[1][kk], gram[1]);
+                        } else {
+                            // fp16 x = hi + lo exactly in bf16; x_lo meets the
+                            // hi B columns only (x_lo * B_lo is below 2^-16 of
+                            // the product).
+                            u32x4_t xh[2], xl[2];
+#pragma unroll
+                            for (int r = 0; r < 2; ++r) {
+                                float fx[8];
+                                unpack8<false>(af[r][kk], fx);
+                                split_f16_to_bf16(fx, xh[r], xl[r]);
+                            }
+#pragma unroll
+                            for (int t = 0; t < NT; ++t) {
+                                const u32x4_t b = bsh[sl][ksl * NT + t][lane];
+#pragma unroll
+                                for (int r = 0; r < 2; ++r) {
+                                    acc[r][C::acc(t)] = mfma16(xh[r], b, acc[r][C::acc(t)]);
+                                    if (C::hi_tile(t)) {
+                                        acc[r][C::acc(t)] = mfma16(xl[r], b, acc[r][C::acc(t)]);
+                                    }
+                                }
+                            }
+                            gram[0] = mfma16_f16(af[0][kk], af[0][kk], gram[0]);
+                            gram[1] = mfma16_f16(af[1][kk], af[1][kk], gram[1]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    // Loads of the stages past the K-range may still be in flight.
+    __builtin_amdgcn_s_waitcnt(0);
+    if (vrows == 0) {
+        return;
+    }
+
+    // C fragment: lane l, register e holds row 4(l >> 4) + e, column l & 15
+    // of its 16 x 16 tile.
+    float *dst = a.partial + ((int64_t)kr * a.T + r0) * (M + 1);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = 16 * r + 4 * (lane >> 4) + e;
+            const bool ok = row < vrows;
+            float *drow = dst + (int64_t)row * (M + 1);
+#pragma unroll
+            for (int t = 0; t < Q; ++t) {
+                if (ok) {
+                    drow[16 * t + (lane & 15)] = acc[r][t][e];
+                }
+            }
+            if constexpr (C::kHalf) {
+                // hi in lanes 0-7 of each 16, lo of the same column 8 lanes up.
+                const float v = acc[r][Q][e];
+                const float lo = __shfl_down(v, 8, 16);
+                if (ok && (lane & 15) < 8) {
+                    drow[16 * Q + (lane & 7)] = v + lo;
+                }
+            }
+            // Diagonal of the Gram tile: the row's sum of squares.
+            if (ok && (lane & 15) == 4 * (lane >> 4) + e) {
+                drow[M] = gram[r][e];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// rows_epilogue: one workgroup per row.
+// ---------------------------------------------------------------------------
+struct RowsEpiArgs {
+    const uint16_t *x;
+    const float *partial;  // [S][T][M + 1]
+    const float *alpha;
+    const float *bias;
+    uint16_t *hIn;
+    float *hPost;
+    float *hRes;
+    float *hPre;
+    int64_t T;
+    int64_t D;
+    int S;
+    float normEps;
+    float hcEps;
+    float invFlatDim;
+};
+
+template <int N, bool kBf16>
+__global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs a)
+{
+    constexpr int M = N * N + 2 * N;
+    constexpr int COLS = M + 1;
+    constexpr int G = kEpiThreads / COLS;  // partial-sum groups
+    __shared__ float red[G][COLS];
+    __shared__ float smix[COLS];
+    __shared__ float spre[N];
+
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t DO = a.D / 8;  // column octets
+    const int Di2 = (int)(a.D * 2);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + row * N * a.D, N * Di2);
+    const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.hIn + row * a.D, Di2);
+
+    // First pass of x loads, issued before the partial sums so that both
+    // round trips overlap.  Octets past D read zeros (size-bounded resource).
+    u32x4_t xv[kEpiOct][N];
+#pragma unroll
+    for (int o = 0; o < kEpiOct; ++o) {
+        const int d8 = tid + kEpiThreads * o;
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+            xv[o][s] = load16<0>(xr, s * Di2 + d8 * 16);
+        }
+    }
+
+    // Partial sums: group q sums K-ranges [q*Sg, (q+1)*Sg) of column j in
+    // order; the groups are then added in group order.
+    const int q = tid / COLS;
+    const int j = tid - q * COLS;
+    if (q < G) {
+        const int Sg = (a.S + G - 1) / G;
+        const int sBeg = q * Sg;
+        const int sEnd = min(a.S, sBeg + Sg);
+        const float *src = a.partial + row * COLS + j;
+        const int64_t stride = a.T * COLS;
+        float v = 0.f;
+        int s = sBeg;
+        for (; s + 8 <= sEnd; s += 8) {
+            float t[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                t[i] = src[(int64_t)(s + i) * stride];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v = v + t[i];
+            }
+        }
+        for (; s < sEnd; ++s) {
+            v = v + src[(int64_t)s * stride];
+        }
+        red[q][j] = v;
+    }
+    __syncthreads();
+    if (tid < COLS) {
+        float v = red[0][tid];
+#pragma unroll
+        for (int i = 1; i < G; ++i) {
+            v = v + red[i][tid];
+        }
+        smix[tid] = v;
+    }
+    __syncthreads();
+
+    if (tid < M) {
+        const float invRms = ref_inv_rms(smix[M], a.invFlatDim, a.normEps);
+        const float mix = smix[tid];
+        if (tid < N) {
+            const float sP = invRms * a.alpha[0];
+            const float v = ref_sigmoid(mix * sP, a.bias[tid], a.hcEps);
+            spre[tid] = v;
+            if (a.hPre != nullptr) {
+                a.hPre[row * N + tid] = v;
+            }
+        } else if (tid < 2 * N) {
+            const float sQ = invRms * a.alpha[1];
+            const float v = ref_sigmoid(mix * sQ, a.bias[tid], 0.0f);
+            a.hPost[row * N + (tid - N)] = v * 2.0f;
+        } else {
+            const float sR = invRms * a.alpha[2];
+            const float v = mix * sR;
+            a.hRes[row * (N * N) + (tid - 2 * N)] = v + a.bias[tid];
+        }
+    }
+    __syncthreads();
+
+    float pre[N];
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+        pre[s] = spre[s];
+    }
+    // hIn[d] = RNE(sum over s of pre[s] * x[s][d]), summed in stream order.
+    for (int64_t base = 0; base < DO; base += (int64_t)kEpiThreads * kEpiOct) {
+        if (base > 0) {
+#pragma unroll
+            for (int o = 0; o < kEpiOct; ++o) {
+                const int d8 = (int)base + tid + kEpiThreads * o;
+#pragma unroll
+                for (int s = 0; s < N; ++s) {
+                    xv[o][s] = load16<0>(xr, s * Di2 + d8 * 16);
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 0; o < kEpiOct; ++o) {
+            const int d8 = (int)base + tid + kEpiThreads * o;
+            float acc[8];
+            {
+                float f[8];
+                unpack8<kBf16>(xv[o][0], f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    acc[e] = pre[0] * f[e];
+                }
+            }
+#pragma unroll
+            for (int s = 1; s < N; ++s) {
+                float f[8];
+                unpack8<kBf16>(xv[o][s], f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float p = pre[s] * f[e];
+                    acc[e] = acc[e] + p;
+                }
+            }
+            u32x4_t out;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                out[w] = f32_to_x<kBf16>(acc[2 * w]) | (f32_to_x<kBf16>(acc[2 * w + 1]) << 16);
+            }
+            if (d8 < DO) {
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, out), hr,
+                    d8 * 16, 0, kCpolNt);
+            }
+        }
+    }
+}
+
+template <int N, bool kBf16>
+hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t stream)
+{
+    char *ws = static_cast<char *>(workspace);
+    uint32_t *status = reinterpret_cast<uint32_t *>(ws);
+    u32x4_t *bfrag = reinterpret_cast<u32x4_t *>(ws + p.wsRowsB);
+    float *partial = reinterpret_cast<float *>(ws + p.wsRowsPartial);
+    using C = RowsCols<N>;
+
+    const int64_t prepThreads = (p.K / 32) * C::NA * kWave;
+    hipLaunchKernelGGL((rows_prep_b_kernel<N>), dim3((unsigned)((prepThreads + 255) / 256)),
+                       dim3(256), 0, stream, p.phi, p.hasGamma ? p.gamma : nullptr, bfrag, p.K,
+                       status);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+
+    RowsGemmArgs g;
+    g.x = static_cast<const uint16_t *>(p.x);
+    g.bfrag = bfrag;
+    g.partial = partial;
+    g.T = p.T;
+    g.K = p.K;
+    g.ksPer = p.rowsKsPer;
+    g.S = p.rowsS;
+    g.rowBlocks = p.rowsBlocks;
+    g.nXcd = nXcd;
+    const int items = p.rowsBlocks * p.rowsS;
+    g.perXcd = (items + nXcd - 1) / nXcd;
+    hipLaunchKernelGGL((rows_gemm_kernel<N, kBf16>), dim3((unsigned)(g.perXcd * nXcd)),
+                       dim3(kRW * 64), 0, stream, g);
+    err = hipGetLastError();
+    if (err != hipSuccess) {
+        return err;
+    }
+
+    RowsEpiArgs e;
+    e.x = static_cast<const uint16_t *>(p.x);
+    e.partial = partial;
+    e.alpha = p.alpha;
+    e.bias = p.bias;
+    e.hIn = static_cast<uint16_t *>(p.hIn);
+    e.hPost = p.hPost;
+    e.hRes = p.hRes;
+    e.hPre = p.hasHPre ? p.hPre : nullptr;
+    e.T = p.T;
+    e.D = p.D;
+    e.S = p.rowsS;
+    e.normEps = p.normEps;
+    e.hcEps = p.hcEps;
+    e.invFlatDim = p.invFlatDim;
+    hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16>), dim3((unsigned)p.T), dim3(kEpiThreads), 0,
+                       stream, e);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int rows_block_rows() { return kRowBlock; }
+int rows_stage_ksteps() { return kStageKs; }
+
+hipError_t launch_rows(const Plan &p, void *workspace, int nXcd, hipStream_t stream)
+{
+    switch (p.n) {
+    case 6:
+        return p.isBf16 ? launch_rows_t<6, true>(p, workspace, nXcd, stream)
+                        : launch_rows_t<6, false>(p, workspace, nXcd, stream);
+    case 8:
+        return p.isBf16 ? launch_rows_t<8, true>(p, workspace, nXcd, stream)
+                        : launch_rows_t<8, false>(p, workspace, nXcd, stream);
+    default:
+        return hipErrorNotSupported;
+    }
+}
+
+}  // namespace mhc

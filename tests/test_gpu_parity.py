@@ -310,3 +310,30 @@ def test_shared_workspace_back_to_back(pkg, orc, device, force, expect):
             check(fetch(op), ref, x, True, orc)
     for op in ops:
         op.close()
+
+
+@pytest.mark.parametrize("T,n,D,is_bf16,has_gamma", [
+    (300, 8, 1024, True, True),     # two 256-row blocks, the second with 44 rows
+    (513, 6, 2048, False, True),    # three blocks, the last with one row; fp16 x split
+    (1, 8, 128, True, False),       # one row
+    (2000, 8, 512, True, True),     # eight blocks, short K-ranges
+    (257, 6, 7168, True, False),    # long K (43008): many stages per K-range
+    (96, 8, 2048, False, False),    # fp16, one partial block
+])
+def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
+    """Row-block path (n = 6, 8): ragged row blocks, several K-ranges, fp16 and
+    bf16 x, gamma on and off, against the oracle."""
+    rng = np.random.default_rng(T * 17 + n * 5 + D)
+    K, M = n * D, n * n + 2 * n
+    xf = rng.standard_normal((T, n, D)).astype(np.float32)
+    xf[::7] *= 50.0  # large rows exercise the RMS scale
+    x = to_bits(xf, is_bf16)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.asarray([0.3, -0.2, 0.05], dtype=np.float32)
+    bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
+    _say(f"[rows] T={T} n={n} D={D} bf16={is_bf16} gamma={has_gamma}")
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
+    assert out["path"] == "rows"
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
+    check(out, ref, x, is_bf16, orc)

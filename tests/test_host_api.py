@@ -189,3 +189,47 @@ def test_phase1_is_thread_safe(pkg, lib):
     for t in threads:
         t.join()
     assert not errors
+
+
+def _path(pkg, lib, d, env=None):
+    import os
+
+    mk = lambda v: None if v is None else ctypes.byref(pkg.make_tensor(*v))
+    ws = ctypes.c_uint64(0)
+    exe = ctypes.c_void_p(None)
+    if env is not None:
+        os.environ["MHCPRE_FORCE_PATH"] = env
+    try:
+        st = lib.mhcPreGetWorkspaceSize(mk(d["x"]), mk(d["phi"]), mk(d["alpha"]), mk(d["bias"]),
+                                        mk(d["gamma"]), ctypes.c_float(1e-6), ctypes.c_float(1e-6),
+                                        mk(d["hIn"]), mk(d["hPost"]), mk(d["hRes"]),
+                                        ctypes.byref(ws), ctypes.byref(exe))
+    finally:
+        os.environ.pop("MHCPRE_FORCE_PATH", None)
+    assert st == 0
+    name = ctypes.c_char_p()
+    assert lib.mhcPreExecutorPath(exe, ctypes.byref(name)) == 0
+    lib.mhcPreExecutorDestroy(exe)
+    return name.value.decode()
+
+
+@pytest.mark.parametrize("n,D,S,want", [
+    (4, 7168, 64, "strip"),    # D % 256 == 0, D / 256 <= 31
+    (4, 64, 64, "fused"),      # n = 4, D % 64 == 0, not a strip shape
+    (4, 48, 64, "split"),      # n = 4, D % 64 != 0
+    (8, 7168, 64, "rows"),     # n = 8, K % 128 == 0
+    (8, 8192, 5472, "rows"),
+    (6, 1024, 16, "rows"),     # K = 6144
+    (6, 48, 16, "split"),      # K = 288: not a multiple of 128
+    (8, 16, 16, "rows"),       # K = 128
+])
+def test_path_selection(pkg, lib, n, D, S, want):
+    assert _path(pkg, lib, _descs(pkg, S=S, n=n, D=D)) == want
+
+
+def test_forced_paths(pkg, lib):
+    d = _descs(pkg, S=64, n=8, D=1024)
+    assert _path(pkg, lib, d, env="split") == "split"
+    assert _path(pkg, lib, d, env="rows") == "rows"
+    # A path the shape cannot take is ignored.
+    assert _path(pkg, lib, _descs(pkg, S=16, n=6, D=48), env="rows") == "split"
