@@ -263,38 +263,40 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     if (n == 4 && (D % 256) == 0 && D / 256 <= mhc::strip_max_slices() && T < (int64_t{1} << 24)) {
         p.stripP = static_cast<int>(D / 256);
     }
-    // Rows path (n = 6, 8): 256-row blocks x K-ranges of whole 4-k-step
-    // stages.  The K-range count balances whole waves of 256 workgroups (one
-    // per CU of an MI355X; the count only affects speed) against the partial
-    // traffic: cost ~ rounds * (x bytes of one item) + partial bytes written
-    // and read.  32-bit buffer offsets bound K and the B bytes of a range.
-    if ((n == 6 || n == 8) && (K % 128) == 0 && K < (int64_t{1} << 25)) {
+    // Rows path (n = 6, 8): 256-row blocks x S K-ranges of contiguous
+    // 4-k-step stages (the last range may be shorter).  S balances whole waves of 256
+    // workgroups (one per CU of an MI355X; S only affects speed) against the
+    // partial traffic: cost ~ rounds * (x bytes of one item) + partial bytes
+    // written and read.  32-bit buffer offsets bound K and the B bytes.
+    const int64_t rowsNT = (2 * M) / 16;
+    if ((n == 6 || n == 8) && (K % 128) == 0 && K < (int64_t{1} << 25) &&
+        (K / 32) * rowsNT * 1024 < (int64_t{1} << 31)) {
         const int64_t blockRows = mhc::rows_block_rows();
-        const int64_t stageKs = mhc::rows_stage_ksteps();
         const int64_t blocks = (T + blockRows - 1) / blockRows;
-        const int64_t KS = K / 32;
+        const int64_t NS = K / 32 / mhc::rows_stage_ksteps();
+        const int64_t stageBytes = 32 * 2 * mhc::rows_stage_ksteps();
         constexpr int64_t kSlotsPerRound = 256;
         double best = -1.0;
-        for (int64_t s = 1; s <= KS / stageKs; ++s) {
-            const int64_t ksPer = stageKs * ((KS + stageKs * s - 1) / (stageKs * s));
-            const int64_t S = (KS + ksPer - 1) / ksPer;
-            if (S != s) {
-                continue;
+        for (int64_t S = 1; S <= NS; ++S) {
+            const int64_t perItem = (NS + S - 1) / S;
+            if (S > 1 && (NS + S - 2) / (S - 1) == perItem) {
+                continue;  // same stages per item with fewer ranges; this
+                           // also keeps every range non-empty
             }
             const int64_t rounds = (blocks * S + kSlotsPerRound - 1) / kSlotsPerRound;
             const double cost = static_cast<double>(rounds) * static_cast<double>(std::min(T, blockRows)) *
-                                    static_cast<double>(ksPer) * 64.0 * kSlotsPerRound +
+                                    static_cast<double>(perItem * stageBytes) * kSlotsPerRound +
                                 2.0 * static_cast<double>(S) * static_cast<double>(T) * (M + 1) * 4.0;
             if (best < 0.0 || cost < best) {
                 best = cost;
                 p.rowsS = static_cast<int>(S);
-                p.rowsKsPer = static_cast<int>(ksPer);
             }
         }
-        if (static_cast<int64_t>(p.rowsKsPer) * p.NT * 1024 >= (int64_t{1} << 31)) {
+        p.rowsBlocks = static_cast<int>(blocks);
+        // The epilogue addresses the partials with 32-bit offsets.
+        if (static_cast<int64_t>(p.rowsS) * T * (M + 1) * 4 >= (int64_t{1} << 31)) {
             p.rowsS = 0;
         }
-        p.rowsBlocks = static_cast<int>(blocks);
     }
     p.path = p.stripP > 0 ? mhc::Path::kStrip
                           : (p.fusedP > 0 ? mhc::Path::kFused
@@ -473,7 +475,7 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
     }
     if (!done && p.path == mhc::Path::kRows) {
         executor->lastEpoch.store(next_epoch(), std::memory_order_relaxed);
-        err = mhc::launch_rows(p, workspace, shape.xcds, stream);
+        err = mhc::launch_rows(p, workspace, shape.xcds, shape.cus, stream);
         done = true;
     }
     if (!done) {

@@ -73,10 +73,9 @@ struct Plan {
     int stripTeamsPerXcd = 0;
     int stripGrid = 0;
 
-    // Rows path (n = 6, 8; K % 128 == 0): rowsS K-ranges of rowsKsPer
-    // k-steps over rowsBlocks blocks of 256 rows.
+    // Rows path (n = 6, 8; K % 128 == 0): rowsS K-ranges (contiguous runs
+    // of 4-k-step stages) over rowsBlocks blocks of 256 rows.
     int rowsS = 0;
-    int rowsKsPer = 0;
     int rowsBlocks = 0;
 
     // Workspace layout (byte offsets).  The paths' regions overlap: a
@@ -109,9 +108,9 @@ hipError_t launch_fused(const Plan &plan, void *workspace, uint32_t epoch, hipSt
 
 hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
 
-// Rows path (mhc_pre_rows.hip); nXcd: XCDs of the device (work-item placement
-// only).
-hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, hipStream_t stream);
+// Rows path (mhc_pre_rows.hip); nXcd, nCu: XCDs and CUs of the device
+// (work placement and grid size only).
+hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, int nCu, hipStream_t stream);
 // Rows per work item and k-steps per stage of the rows-path GEMM.
 int rows_block_rows();
 int rows_stage_ksteps();

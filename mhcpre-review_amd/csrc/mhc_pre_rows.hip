@@ -18,11 +18,15 @@
 //                  columns.  Lane l holds k = 32ks + 8(l/16) .. +8.
 //   rows_gemm      split-K GEMM over work items (256-row block, K-range).  A
 //                  workgroup is 8 waves of 32 rows (two 16-row MFMA blocks).
-//                  K-ranges are walked in stages of 4 k-steps: each stage's B
-//                  fragments go into an LDS ring by direct-to-LDS buffer loads
-//                  (each wave copies NT/2 of its 4*NT fragments), its x into a
-//                  register ring as whole 128-byte lines (8 lanes per row), both
-//                  kAhead stages ahead of the MFMAs.  A DPP row_ror:8 turns two
+//                  K is cut into stages of 4 k-steps (two 128-byte lines of a
+//                  row); K-range kr takes a contiguous run of stages.  x is
+//                  read with nontemporal loads (measured on MI355X: 6.4 TB/s
+//                  for this read pattern against 4.9 with default caching or
+//                  with the ranges' stages interleaved).  Each stage's B fragments
+//                  go through registers into an LDS ring (each wave copies
+//                  NT/2 of the 4*NT fragments), its x into a register ring as
+//                  whole 128-byte lines (8 lanes per row), both kAhead stages
+//                  ahead of the MFMAs.  A DPP row_ror:8 turns two
 //                  line registers into the A fragments of two k-steps.  hi and
 //                  lo products accumulate into one fp32 accumulator per mix
 //                  column; a Gram MFMA of the same fragments gives the sum of
@@ -47,19 +51,22 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 namespace mhc {
 namespace {
 
 using namespace dev;
 
-constexpr int kRW = 8;                       // waves per GEMM workgroup
+constexpr int kRW = 8;                       // waves per GEMM workgroup (two per SIMD)
 constexpr int kRowsWave = 32;                // rows per wave (two 16-row MFMA blocks)
 constexpr int kRowBlock = kRW * kRowsWave;   // rows per work item
-constexpr int kStageKs = 4;                  // k-steps per stage: two 128-byte lines of a row
-constexpr int kAhead = 2;                    // stages loading ahead of the MFMAs
-constexpr int kSlots = kAhead + 1;           // ring depth (x registers and B in LDS)
-constexpr int kEpiThreads = 512;             // epilogue workgroup
-constexpr int kEpiOct = 2;                   // hIn column octets per thread per pass
+constexpr int kStageKs = 2;                  // k-steps per stage (kStageKs / 2 lines of a row)
+constexpr int kAhead = 3;                    // stages of x loading ahead of the MFMAs
+constexpr int kXSlots = kAhead + 1;          // x register ring
+constexpr int kBSets = kAhead - 1;           // B staging register sets
+constexpr int kEpiThreads = 256;             // epilogue workgroup
+constexpr int kEpiOct = 4;                   // hIn column octets per thread per pass
 
 // Column tiles of the B operand and the accumulator tile each one adds into.
 template <int N>
@@ -74,7 +81,7 @@ struct RowsCols {
     static constexpr bool hi_tile(int t) { return t < Q || t == 2 * Q; }
 };
 
-constexpr int kCpolNt = 2;  // nontemporal: hIn is written once
+constexpr int kCpolNt = 2;  // nontemporal: x is streamed, hIn written once
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int bytes)
 {
@@ -200,8 +207,8 @@ struct RowsGemmArgs {
     float *partial;  // [S][T][M + 1]
     int64_t T;
     int64_t K;
-    int ksPer;       // k-steps per K-range (a multiple of kStageKs)
-    int S;           // K-ranges
+    int NS;          // stages of K (K / 32 / kStageKs)
+    int S;           // K-ranges of ceil(NS / S) stages (the last may be shorter)
     int rowBlocks;   // 256-row blocks
     int perXcd;      // item slots per XCD
     int nXcd;
@@ -215,12 +222,13 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
     constexpr int NT = C::NT;
     constexpr int NA = C::NA;
     constexpr int Q = C::Q;
-    constexpr int SF = kStageKs * NT;  // B fragments per stage
-    constexpr int NB = SF / kRW;       // of which each wave copies NB
-    static_assert(SF % kRW == 0, "each wave copies the same number of B fragments");
-    constexpr int kXLoads = 8;         // x line loads per wave and stage
-    constexpr int kUnroll = kSlots;    // steps per loop trip (static ring slots)
-    __shared__ u32x4_t bsh[kSlots][SF][kWave];
+    constexpr int kLines = kStageKs / 2;      // 128-byte lines of a row per stage
+    constexpr int SF = kStageKs * NT;         // B fragments per stage
+    constexpr int NB = (SF + kRW - 1) / kRW;  // fragments each wave copies (some waves one fewer)
+    constexpr int kXLoads = 4 * kLines;       // x line loads per wave and stage
+    constexpr int kUnroll = kXSlots;          // steps per loop trip: every ring index static
+    static_assert(kUnroll % kBSets == 0 && kUnroll % 2 == 0, "static ring indices");
+    __shared__ u32x4_t bsh[2][SF][kWave];     // B of stages s and s + 1
 
     const int lane = threadIdx.x & 63;
     // Wave-uniform (scalar) wave index: the buffer resources built from it
@@ -233,9 +241,9 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
     }
     const int rb = f % a.rowBlocks;
     const int kr = f / a.rowBlocks;
-    const int KS = (int)(a.K / 32);
-    const int ks0 = kr * a.ksPer;
-    const int nst = min(a.ksPer, KS - ks0) / kStageKs;
+    const int per = (a.NS + a.S - 1) / a.S;
+    const int gs0 = kr * per;                 // first stage of this K-range
+    const int nst = min(per, a.NS - gs0);     // its stages (at least one)
 
     // x of this wave's 32 rows, through a resource that covers the valid
     // rows only: loads of rows past T return zeros.
@@ -243,13 +251,11 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
     const int vrows = (int)max((int64_t)0, min((int64_t)kRowsWave, a.T - r0));
     const int K2 = (int)(a.K * 2);  // row stride in bytes
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + (vrows > 0 ? r0 * a.K : 0), vrows * K2);
-    const int xLane = (lane & 7) * K2 + 2 * (8 * (lane >> 4) + 32 * ((lane >> 3) & 1)) + ks0 * 64;
-    // B fragments of this K-range.
-    const __amdgpu_buffer_rsrc_t br =
-        make_rsrc(a.bfrag + (int64_t)ks0 * NT * kWave, nst * SF * kWave * 16);
+    const int xLane = (lane & 7) * K2 + 2 * (8 * (lane >> 4) + 32 * ((lane >> 3) & 1));
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bfrag, a.NS * SF * kWave * 16);
 
-    u32x4_t xs[kSlots][4][2];  // [slot][8-row group][line of the stage]
-    u32x4_t bst[NB];           // B fragments of a stage on their way to LDS
+    u32x4_t xs[kXSlots][4][kLines];  // [slot][8-row group][line of the stage]
+    u32x4_t bst[kBSets][NB];         // B fragments of a stage on their way to LDS
 
     // Per-lane offsets are loop-invariant registers and the stage's part of
     // each address is a scalar offset.
@@ -260,38 +266,44 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
         xOff[h] = xLane + 8 * h * K2;
     }
 
-    // Stage s's loads: its B fragments into the staging registers (they go
-    // to LDS one step later, just before the next stage's B reuses the
-    // registers), then its x lines into ring slot s mod kSlots.
-    // Every stage issues the same loads in the same order, live or not:
-    // stages past the K-range read through size-0 resources, so the counter
-    // waits below stay exact.
-    auto issue = [&](int s, u32x4_t(&bd)[NB], u32x4_t(&xd)[4][2]) {
+    // Stage s's loads: its B fragments into staging set s mod kBSets, then
+    // its x lines into ring slot s mod kXSlots.  Every stage issues the same
+    // loads in the same order, live or not: stages past the K-range (and a
+    // wave's fragment slots past SF) read through size-0 resources, so the
+    // counter waits below stay exact.
+    auto issue = [&](int s, u32x4_t(&bd)[NB], u32x4_t(&xd)[4][kLines]) {
         const bool live = s < nst;
-        const __amdgpu_buffer_rsrc_t bq = live ? br : make_rsrc(a.bfrag, 0);
-        const __amdgpu_buffer_rsrc_t xq = live ? xr : make_rsrc(a.x, 0);
+        const int gs = gs0 + s;  // stage of K
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
+            const int fr = w + kRW * i;
+            const __amdgpu_buffer_rsrc_t bq = (live && fr < SF) ? br : make_rsrc(a.bfrag, 0);
             bd[i] = __builtin_bit_cast(
-                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(bq, bLane, (s * SF + kRW * i) * (kWave * 16), 0));
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(bq, bLane, (gs * SF + kRW * i) * (kWave * 16), 0));
         }
-        // Keep the B loads ahead of the x lines: waiting for them next step
-        // must not wait for this stage's x.
+        // Keep the B loads ahead of the x lines in the (in-order) load
+        // counter: waiting for them must not wait for this stage's x.
         __builtin_amdgcn_sched_barrier(0);
+        const __amdgpu_buffer_rsrc_t xq = live ? xr : make_rsrc(a.x, 0);
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
+            for (int c = 0; c < kLines; ++c) {
                 xd[h][c] = __builtin_bit_cast(
                     u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xq, xOff[h] + 128 * c,
-                                                                   s * (kStageKs * 64), 0));
+                                                                   gs * (kStageKs * 64), kCpolNt));
             }
         }
+        // Stages stay in issue order in the load counter.
+        __builtin_amdgcn_sched_barrier(0);
     };
     auto stash = [&](int sl, const u32x4_t(&bd)[NB]) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            bsh[sl][w + kRW * i][lane] = bd[i];
+            const int fr = w + kRW * i;
+            if (fr < SF) {
+                bsh[sl][fr][lane] = bd[i];
+            }
         }
     };
 
@@ -306,33 +318,48 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
         }
     }
 
-    // Prologue: stages 0 and 1 in flight, stage 0's B in LDS.
-    static_assert(kAhead == 2 && kSlots == 3, "ring geometry");
-    issue(0, bst, xs[0]);
+    // Prologue: stages 0 .. kAhead - 1 in flight, stage 0's B in LDS.
+    issue(0, bst[0], xs[0]);
     wait_vm<kXLoads>();
-    stash(0, bst);
-    issue(1, bst, xs[1]);
+    stash(0, bst[0]);
+#pragma unroll
+    for (int s = 1; s < kAhead; ++s) {
+        issue(s, bst[s % kBSets], xs[s]);
+    }
 
     // Step s: x of stage s and B of stage s + 1 have arrived once only the
-    // x lines of stage s + 1 may still be in flight.  The barrier makes every
+    // loads issued after B(s + 1) -- x of stage s + 1 and stages s + 2 ..
+    // s + kAhead - 1 -- may still be in flight.  The barrier makes every
     // wave's stash of B(s) visible and tells every wave that all reads of
-    // slot (s + 1) mod 3 (last read at step s - 2) are done; B(s + 1) goes
-    // there, and stage s + 2's loads go out behind it.
-    // The trip count is rounded up to whole trips: the stages past the
-    // K-range read zeros for both x and B, and add nothing.
+    // LDS slot (s + 1) mod 2 (stage s - 1) are done; B(s + 1) goes there,
+    // and stage s + kAhead's loads go out into the staging set and ring slot
+    // just freed.  The trip count is rounded up to whole trips: the stages
+    // past the K-range read zeros for both x and B, and add nothing.
     const int nstTrips = (nst + kUnroll - 1) / kUnroll * kUnroll;
     for (int s0 = 0; s0 < nstTrips; s0 += kUnroll) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int s = s0 + u;
-            const int sl = u % kSlots;
-            wait_vm<kXLoads>();
+            const int sl = u % kXSlots;
+            const int bl = u % 2;
+            wait_vm<kXLoads + (kAhead - 2) * (NB + kXLoads)>();
             lds_barrier();
-            stash((u + 1) % kSlots, bst);
-            issue(s + 2, bst, xs[(u + 2) % kSlots]);
+            stash((u + 1) % 2, bst[(u + 1) % kBSets]);
+            issue(s + kAhead, bst[(u + kAhead) % kBSets], xs[(u + kAhead) % kXSlots]);
             if (vrows > 0) {
+                // All of the stage's B fragments are read before its MFMAs,
+                // so the LDS latency is paid once per stage.
+                u32x4_t bf[kStageKs][NT];
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
+                for (int ksl = 0; ksl < kStageKs; ++ksl) {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        bf[ksl][t] = bsh[bl][ksl * NT + t][lane];
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int c = 0; c < kLines; ++c) {
                     u32x4_t af[2][2];  // [16-row block][k-step of the line]
                     lines_to_frags(xs[sl][0][c], xs[sl][1][c], af[0][0], af[0][1]);
                     lines_to_frags(xs[sl][2][c], xs[sl][3][c], af[1][0], af[1][1]);
@@ -342,7 +369,7 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
                         if constexpr (kBf16) {
 #pragma unroll
                             for (int t = 0; t < NT; ++t) {
-                                const u32x4_t b = bsh[sl][ksl * NT + t][lane];
+                                const u32x4_t b = bf[ksl][t];
                                 acc[0][C::acc(t)] = mfma16(af[0][kk], b, acc[0][C::acc(t)]);
                                 acc[1][C::acc(t)] = mfma16(af[1][kk], b, acc[1][C::acc(t)]);
                             }
@@ -361,7 +388,7 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
                             }
 #pragma unroll
                             for (int t = 0; t < NT; ++t) {
-                                const u32x4_t b = bsh[sl][ksl * NT + t][lane];
+                                const u32x4_t b = bf[ksl][t];
 #pragma unroll
                                 for (int r = 0; r < 2; ++r) {
                                     acc[r][C::acc(t)] = mfma16(xh[r], b, acc[r][C::acc(t)]);
@@ -417,7 +444,9 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// rows_epilogue: one workgroup per row.
+// rows_epilogue: one workgroup of 256 threads per row; each thread holds 4
+// column octets of all n streams, so one row's x (up to D = 8192) is in
+// flight at once and a CU keeps several rows in flight.
 // ---------------------------------------------------------------------------
 struct RowsEpiArgs {
     const uint16_t *x;
@@ -452,16 +481,17 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
     const int Di2 = (int)(a.D * 2);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + row * N * a.D, N * Di2);
     const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.hIn + row * a.D, Di2);
+    const int xLane = tid * 16;
 
     // First pass of x loads, issued before the partial sums so that both
-    // round trips overlap.  Octets past D read zeros (size-bounded resource).
+    // round trips overlap.  Octets past D read other streams' data or zeros
+    // (size-bounded resource) and are not stored.
     u32x4_t xv[kEpiOct][N];
 #pragma unroll
     for (int o = 0; o < kEpiOct; ++o) {
-        const int d8 = tid + kEpiThreads * o;
 #pragma unroll
         for (int s = 0; s < N; ++s) {
-            xv[o][s] = load16<0>(xr, s * Di2 + d8 * 16);
+            xv[o][s] = load16<kCpolNt>(xr, xLane + o * (kEpiThreads * 16) + s * Di2);
         }
     }
 
@@ -476,20 +506,20 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         const float *src = a.partial + row * COLS + j;
         const int64_t stride = a.T * COLS;
         float v = 0.f;
-        int s = sBeg;
-        for (; s + 8 <= sEnd; s += 8) {
+        int sk = sBeg;
+        for (; sk + 8 <= sEnd; sk += 8) {
             float t[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                t[i] = src[(int64_t)(s + i) * stride];
+                t[i] = src[(int64_t)(sk + i) * stride];
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 v = v + t[i];
             }
         }
-        for (; s < sEnd; ++s) {
-            v = v + src[(int64_t)s * stride];
+        for (; sk < sEnd; ++sk) {
+            v = v + src[(int64_t)sk * stride];
         }
         red[q][j] = v;
     }
@@ -536,10 +566,9 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         if (base > 0) {
 #pragma unroll
             for (int o = 0; o < kEpiOct; ++o) {
-                const int d8 = (int)base + tid + kEpiThreads * o;
 #pragma unroll
                 for (int s = 0; s < N; ++s) {
-                    xv[o][s] = load16<0>(xr, s * Di2 + d8 * 16);
+                    xv[o][s] = load16<kCpolNt>(xr, (int)(base * 16) + xLane + o * (kEpiThreads * 16) + s * Di2);
                 }
             }
         }
@@ -580,7 +609,7 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
 }
 
 template <int N, bool kBf16>
-hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t stream)
+hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, int nCu, hipStream_t stream)
 {
     char *ws = static_cast<char *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(ws);
@@ -603,7 +632,7 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
     g.partial = partial;
     g.T = p.T;
     g.K = p.K;
-    g.ksPer = p.rowsKsPer;
+    g.NS = (int)(p.K / 32 / kStageKs);
     g.S = p.rowsS;
     g.rowBlocks = p.rowsBlocks;
     g.nXcd = nXcd;
@@ -631,6 +660,7 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
     e.normEps = p.normEps;
     e.hcEps = p.hcEps;
     e.invFlatDim = p.invFlatDim;
+    (void)nCu;
     hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16>), dim3((unsigned)p.T), dim3(kEpiThreads), 0,
                        stream, e);
     return hipGetLastError();
@@ -641,15 +671,15 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
 int rows_block_rows() { return kRowBlock; }
 int rows_stage_ksteps() { return kStageKs; }
 
-hipError_t launch_rows(const Plan &p, void *workspace, int nXcd, hipStream_t stream)
+hipError_t launch_rows(const Plan &p, void *workspace, int nXcd, int nCu, hipStream_t stream)
 {
     switch (p.n) {
     case 6:
-        return p.isBf16 ? launch_rows_t<6, true>(p, workspace, nXcd, stream)
-                        : launch_rows_t<6, false>(p, workspace, nXcd, stream);
+        return p.isBf16 ? launch_rows_t<6, true>(p, workspace, nXcd, nCu, stream)
+                        : launch_rows_t<6, false>(p, workspace, nXcd, nCu, stream);
     case 8:
-        return p.isBf16 ? launch_rows_t<8, true>(p, workspace, nXcd, stream)
-                        : launch_rows_t<8, false>(p, workspace, nXcd, stream);
+        return p.isBf16 ? launch_rows_t<8, true>(p, workspace, nXcd, nCu, stream)
+                        : launch_rows_t<8, false>(p, workspace, nXcd, nCu, stream);
     default:
         return hipErrorNotSupported;
     }
