@@ -77,6 +77,9 @@ struct Plan {
     // of 4-k-step stages) over rowsBlocks blocks of 256 rows.
     int rowsS = 0;
     int rowsBlocks = 0;
+    // Small batches (T <= rows_small_rows()): one GEMM workgroup per K-range
+    // of rows_small_ksteps() k-steps, B built from phi in registers, no prep.
+    bool rowsSmall = false;
 
     // Workspace layout (byte offsets).  The paths' regions overlap: a
     // workspace holds one launch at a time.
@@ -114,6 +117,9 @@ hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, int nCu, hip
 // Rows per work item and k-steps per stage of the rows-path GEMM.
 int rows_block_rows();
 int rows_stage_ksteps();
+// Largest batch of the small-batch GEMM and k-steps per workgroup there.
+int rows_small_rows();
+int rows_small_ksteps();
 
 // Workgroups of the strip kernel that can be resident per CU (x numCUs), or
 // -1 if the plan has no strip kernel.

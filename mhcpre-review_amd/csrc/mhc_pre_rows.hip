@@ -65,8 +65,9 @@ constexpr int kStageKs = 2;                  // k-steps per stage (kStageKs / 2 
 constexpr int kAhead = 3;                    // stages of x loading ahead of the MFMAs
 constexpr int kXSlots = kAhead + 1;          // x register ring
 constexpr int kBSets = kAhead - 1;           // B staging register sets
-constexpr int kEpiThreads = 256;             // epilogue workgroup
-constexpr int kEpiOct = 4;                   // hIn column octets per thread per pass
+constexpr int kSmallRows = 64;               // small-batch GEMM: rows held by every wave
+constexpr int kSmallWaves = 4;               // small-batch GEMM: waves splitting a K-range
+constexpr int kSmallKs = 2;                  // small-batch GEMM: k-steps per wave
 
 // Column tiles of the B operand and the accumulator tile each one adds into.
 template <int N>
@@ -444,6 +445,186 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// rows_small: decode-shaped batches (T <= 64).  One workgroup per K-range of
+// kSmallWaves * kSmallKs k-steps; each wave takes kSmallKs of them for all T
+// rows (four 16-row blocks, rows past T read as zeros) and builds its B
+// fragments from phi and gamma in registers, so no prepared copy of B is
+// written or read: with one row block, every element of B is used once.
+// The waves' partial sums meet in LDS and are added in wave order.
+// ---------------------------------------------------------------------------
+struct RowsSmallArgs {
+    const uint16_t *x;
+    const float *phi;
+    const float *gamma;
+    float *partial;    // [S][T][M + 1]
+    uint32_t *status;  // low half of the device status word
+    int64_t T;
+    int64_t K;
+};
+
+template <int N, bool kBf16>
+__global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallArgs a)
+{
+    using C = RowsCols<N>;
+    constexpr int M = C::M;
+    constexpr int NA = C::NA;
+    constexpr int Q = C::Q;
+    constexpr int COLS = M + 1;
+    constexpr int RB = kSmallRows / 16;
+    __shared__ float red[kSmallWaves][kSmallRows][COLS];
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kr = blockIdx.x;
+    const int T = (int)a.T;
+    if (kr == 0 && threadIdx.x == 0) {
+        *a.status = kDeviceOk;
+    }
+    const int K2 = (int)(a.K * 2);
+    const int64_t ks0 = ((int64_t)kr * kSmallWaves + w) * kSmallKs;  // first k-step of this wave
+
+    // A fragments straight in MFMA layout: lane l holds row 16r + (l & 15)
+    // and the 8 k at 8(l >> 4) of its k-step.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, T * K2);
+    u32x4_t xa[kSmallKs][RB];
+#pragma unroll
+    for (int kk = 0; kk < kSmallKs; ++kk) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            xa[kk][r] = load16<kCpolNt>(xr, (16 * r + (lane & 15)) * K2 +
+                                                (int)((ks0 + kk) * 64) + 16 * (lane >> 4));
+        }
+    }
+    // phi (and gamma) for the B fragments: accumulator tile ta covers mix
+    // columns 16ta + (l & 15); the half tile's lanes 8-15 hold the lo half
+    // of the column of lanes 0-7.
+    f32x4_t ph[kSmallKs][NA][2];
+    f32x4_t gm[kSmallKs][2];
+#pragma unroll
+    for (int kk = 0; kk < kSmallKs; ++kk) {
+        const int64_t k0 = (ks0 + kk) * 32 + 8 * (lane >> 4);
+#pragma unroll
+        for (int ta = 0; ta < NA; ++ta) {
+            const int j = ta < Q ? 16 * ta + (lane & 15) : 16 * Q + (lane & 7);
+            const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + k0);
+            ph[kk][ta][0] = src[0];
+            ph[kk][ta][1] = src[1];
+        }
+        const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(a.gamma != nullptr ? a.gamma + k0 : a.phi);
+        gm[kk][0] = gsrc[0];
+        gm[kk][1] = gsrc[1];
+    }
+
+    f32x4_t acc[RB][NA];
+    f32x4_t gram[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        gram[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < NA; ++t) {
+            acc[r][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    const bool hasGamma = a.gamma != nullptr;
+#pragma unroll
+    for (int kk = 0; kk < kSmallKs; ++kk) {
+        u32x4_t xh[RB], xl[RB];
+        if constexpr (!kBf16) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                float fx[8];
+                unpack8<false>(xa[kk][r], fx);
+                split_f16_to_bf16(fx, xh[r], xl[r]);
+            }
+        }
+#pragma unroll
+        for (int ta = 0; ta < NA; ++ta) {
+            float hi[8], lo[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float b = ph[kk][ta][e >> 2][e & 3];
+                if (hasGamma) {
+                    b = b * gm[kk][e >> 2][e & 3];
+                }
+                hi[e] = bf16_bits_to_f32(f32_to_bf16_bits(b));
+                lo[e] = b - hi[e];
+            }
+            const u32x4_t bh = pack8_bf16(hi);
+            const u32x4_t bl = pack8_bf16(lo);
+            if (ta < Q) {
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    if constexpr (kBf16) {
+                        acc[r][ta] = mfma16(xa[kk][r], bh, acc[r][ta]);
+                        acc[r][ta] = mfma16(xa[kk][r], bl, acc[r][ta]);
+                    } else {
+                        acc[r][ta] = mfma16(xh[r], bh, acc[r][ta]);
+                        acc[r][ta] = mfma16(xh[r], bl, acc[r][ta]);
+                        acc[r][ta] = mfma16(xl[r], bh, acc[r][ta]);
+                    }
+                }
+            } else {
+                // Half tile: hi in lanes 0-7 of each 16, lo in lanes 8-15.
+                const u32x4_t bq = (lane & 15) < 8 ? bh : bl;
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    if constexpr (kBf16) {
+                        acc[r][ta] = mfma16(xa[kk][r], bq, acc[r][ta]);
+                    } else {
+                        acc[r][ta] = mfma16(xh[r], bq, acc[r][ta]);
+                        acc[r][ta] = mfma16(xl[r], bq, acc[r][ta]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            if constexpr (kBf16) {
+                gram[r] = mfma16(xa[kk][r], xa[kk][r], gram[r]);
+            } else {
+                gram[r] = mfma16_f16(xa[kk][r], xa[kk][r], gram[r]);
+            }
+        }
+    }
+
+    // This wave's sums into LDS (C fragment: lane l, register e holds row
+    // 4(l >> 4) + e, column l & 15 of its tile).
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = 16 * r + 4 * (lane >> 4) + e;
+#pragma unroll
+            for (int t = 0; t < Q; ++t) {
+                red[w][row][16 * t + (lane & 15)] = acc[r][t][e];
+            }
+            if constexpr (C::kHalf) {
+                const float v = acc[r][Q][e];
+                const float lo = __shfl_down(v, 8, 16);
+                if ((lane & 15) < 8) {
+                    red[w][row][16 * Q + (lane & 7)] = v + lo;
+                }
+            }
+            if ((lane & 15) == 4 * (lane >> 4) + e) {
+                red[w][row][M] = gram[r][e];
+            }
+        }
+    }
+    __syncthreads();
+    float *dst = a.partial + (int64_t)kr * a.T * COLS;
+    for (int idx = threadIdx.x; idx < T * COLS; idx += kSmallWaves * 64) {
+        const int r = idx / COLS;
+        const int c = idx - r * COLS;
+        float v = red[0][r][c];
+#pragma unroll
+        for (int i = 1; i < kSmallWaves; ++i) {
+            v = v + red[i][r][c];
+        }
+        dst[idx] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // rows_epilogue: one workgroup of 256 threads per row; each thread holds 4
 // column octets of all n streams, so one row's x (up to D = 8192) is in
 // flight at once and a CU keeps several rows in flight.
@@ -465,7 +646,7 @@ struct RowsEpiArgs {
     float invFlatDim;
 };
 
-template <int N, bool kBf16>
+template <int N, bool kBf16, int kEpiThreads, int kEpiOct>
 __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs a)
 {
     constexpr int M = N * N + 2 * N;
@@ -482,6 +663,11 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + row * N * a.D, N * Di2);
     const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.hIn + row * a.D, Di2);
     const int xLane = tid * 16;
+
+    // bias and alpha for this thread's output column, loaded up front so
+    // that their round trip overlaps the others.
+    const float biasJ = tid < M ? a.bias[tid] : 0.f;
+    const float alphaJ = tid < N ? a.alpha[0] : (tid < 2 * N ? a.alpha[1] : a.alpha[2]);
 
     // First pass of x loads, issued before the partial sums so that both
     // round trips overlap.  Octets past D read other streams' data or zeros
@@ -537,21 +723,19 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
     if (tid < M) {
         const float invRms = ref_inv_rms(smix[M], a.invFlatDim, a.normEps);
         const float mix = smix[tid];
+        const float sc = invRms * alphaJ;
         if (tid < N) {
-            const float sP = invRms * a.alpha[0];
-            const float v = ref_sigmoid(mix * sP, a.bias[tid], a.hcEps);
+            const float v = ref_sigmoid(mix * sc, biasJ, a.hcEps);
             spre[tid] = v;
             if (a.hPre != nullptr) {
                 a.hPre[row * N + tid] = v;
             }
         } else if (tid < 2 * N) {
-            const float sQ = invRms * a.alpha[1];
-            const float v = ref_sigmoid(mix * sQ, a.bias[tid], 0.0f);
+            const float v = ref_sigmoid(mix * sc, biasJ, 0.0f);
             a.hPost[row * N + (tid - N)] = v * 2.0f;
         } else {
-            const float sR = invRms * a.alpha[2];
-            const float v = mix * sR;
-            a.hRes[row * (N * N) + (tid - 2 * N)] = v + a.bias[tid];
+            const float v = mix * sc;
+            a.hRes[row * (N * N) + (tid - 2 * N)] = v + biasJ;
         }
     }
     __syncthreads();
@@ -611,35 +795,49 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
 template <int N, bool kBf16>
 hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, int nCu, hipStream_t stream)
 {
+    (void)nCu;
     char *ws = static_cast<char *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(ws);
     u32x4_t *bfrag = reinterpret_cast<u32x4_t *>(ws + p.wsRowsB);
     float *partial = reinterpret_cast<float *>(ws + p.wsRowsPartial);
     using C = RowsCols<N>;
+    hipError_t err = hipSuccess;
 
-    const int64_t prepThreads = (p.K / 32) * C::NA * kWave;
-    hipLaunchKernelGGL((rows_prep_b_kernel<N>), dim3((unsigned)((prepThreads + 255) / 256)),
-                       dim3(256), 0, stream, p.phi, p.hasGamma ? p.gamma : nullptr, bfrag, p.K,
-                       status);
-    hipError_t err = hipGetLastError();
-    if (err != hipSuccess) {
-        return err;
+    if (p.rowsSmall) {
+        RowsSmallArgs sa;
+        sa.x = static_cast<const uint16_t *>(p.x);
+        sa.phi = p.phi;
+        sa.gamma = p.hasGamma ? p.gamma : nullptr;
+        sa.partial = partial;
+        sa.status = status;
+        sa.T = p.T;
+        sa.K = p.K;
+        hipLaunchKernelGGL((rows_small_kernel<N, kBf16>), dim3((unsigned)p.rowsS),
+                           dim3(kSmallWaves * 64), 0, stream, sa);
+    } else {
+        const int64_t prepThreads = (p.K / 32) * C::NA * kWave;
+        hipLaunchKernelGGL((rows_prep_b_kernel<N>), dim3((unsigned)((prepThreads + 255) / 256)),
+                           dim3(256), 0, stream, p.phi, p.hasGamma ? p.gamma : nullptr, bfrag, p.K,
+                           status);
+        err = hipGetLastError();
+        if (err != hipSuccess) {
+            return err;
+        }
+        RowsGemmArgs g;
+        g.x = static_cast<const uint16_t *>(p.x);
+        g.bfrag = bfrag;
+        g.partial = partial;
+        g.T = p.T;
+        g.K = p.K;
+        g.NS = (int)(p.K / 32 / kStageKs);
+        g.S = p.rowsS;
+        g.rowBlocks = p.rowsBlocks;
+        g.nXcd = nXcd;
+        const int items = p.rowsBlocks * p.rowsS;
+        g.perXcd = (items + nXcd - 1) / nXcd;
+        hipLaunchKernelGGL((rows_gemm_kernel<N, kBf16>), dim3((unsigned)(g.perXcd * nXcd)),
+                           dim3(kRW * 64), 0, stream, g);
     }
-
-    RowsGemmArgs g;
-    g.x = static_cast<const uint16_t *>(p.x);
-    g.bfrag = bfrag;
-    g.partial = partial;
-    g.T = p.T;
-    g.K = p.K;
-    g.NS = (int)(p.K / 32 / kStageKs);
-    g.S = p.rowsS;
-    g.rowBlocks = p.rowsBlocks;
-    g.nXcd = nXcd;
-    const int items = p.rowsBlocks * p.rowsS;
-    g.perXcd = (items + nXcd - 1) / nXcd;
-    hipLaunchKernelGGL((rows_gemm_kernel<N, kBf16>), dim3((unsigned)(g.perXcd * nXcd)),
-                       dim3(kRW * 64), 0, stream, g);
     err = hipGetLastError();
     if (err != hipSuccess) {
         return err;
@@ -660,15 +858,22 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, int nCu, hipS
     e.normEps = p.normEps;
     e.hcEps = p.hcEps;
     e.invFlatDim = p.invFlatDim;
-    (void)nCu;
-    hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16>), dim3((unsigned)p.T), dim3(kEpiThreads), 0,
-                       stream, e);
+    // Many K-ranges (small batches): more threads share each row's sums.
+    if (p.rowsS > 32) {
+        hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16, 1024, 1>), dim3((unsigned)p.T), dim3(1024),
+                           0, stream, e);
+    } else {
+        hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16, 256, 4>), dim3((unsigned)p.T), dim3(256),
+                           0, stream, e);
+    }
     return hipGetLastError();
 }
 
 }  // namespace
 
 int rows_block_rows() { return kRowBlock; }
+int rows_small_rows() { return kSmallRows; }
+int rows_small_ksteps() { return kSmallWaves * kSmallKs; }
 int rows_stage_ksteps() { return kStageKs; }
 
 hipError_t launch_rows(const Plan &p, void *workspace, int nXcd, int nCu, hipStream_t stream)

@@ -319,6 +319,9 @@ def test_shared_workspace_back_to_back(pkg, orc, device, force, expect):
     (2000, 8, 512, True, True),     # eight blocks, short K-ranges
     (257, 6, 7168, True, False),    # long K (43008): many stages per K-range
     (96, 8, 2048, False, False),    # fp16, one partial block
+    (64, 6, 1024, True, True),      # small-batch GEMM (T <= 64): B built from phi in registers
+    (40, 8, 4096, True, True),      # small-batch GEMM, rows past T in the last 16-row block
+    (2, 6, 2048, False, False),     # small-batch GEMM, fp16, two rows
 ])
 def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     """Row-block path (n = 6, 8): ragged row blocks, several K-ranges, fp16 and
