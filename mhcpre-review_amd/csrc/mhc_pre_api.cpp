@@ -269,7 +269,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     // partial traffic: cost ~ rounds * (x bytes of one item) + partial bytes
     // written and read.  32-bit buffer offsets bound K and the B bytes.
     const int64_t rowsNT = (2 * M) / 16;
-    if ((n == 6 || n == 8) && (K % 128) == 0 && K < (int64_t{1} << 25) &&
+    if ((K % 128) == 0 && K < (int64_t{1} << 25) &&
         (K / 32) * rowsNT * 1024 < (int64_t{1} << 31)) {
         const int64_t blockRows = mhc::rows_block_rows();
         const int64_t blocks = (T + blockRows - 1) / blockRows;
@@ -306,9 +306,21 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             p.rowsS = 0;
         }
     }
-    p.path = p.stripP > 0 ? mhc::Path::kStrip
-                          : (p.fusedP > 0 ? mhc::Path::kFused
-                                          : (p.rowsS > 0 ? mhc::Path::kRows : mhc::Path::kSplit));
+    if (n == 4) {
+        // Small n = 4 batches (T <= 128) take the rows path: the persistent
+        // kernels' fixed cost (every workgroup builds its B slice, a team
+        // works through its few tiles one after another) exceeds the rows
+        // path's two or three short launches there (measured on MI355X:
+        // 15-17 us against 19 us at D = 4096 and 7168, 12 us against 27 us at
+        // D = 256).  From T = 512 on the strip kernel is faster.
+        p.path = p.stripP > 0 ? mhc::Path::kStrip
+                              : (p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit);
+        if (p.rowsS > 0 && T <= 128) {
+            p.path = mhc::Path::kRows;
+        }
+    } else {
+        p.path = p.rowsS > 0 ? mhc::Path::kRows : mhc::Path::kSplit;
+    }
     if (const char *force = std::getenv("MHCPRE_FORCE_PATH")) {
         if (std::strcmp(force, "split") == 0) {
             p.path = mhc::Path::kSplit;
@@ -316,6 +328,8 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             p.path = mhc::Path::kFused;
         } else if (std::strcmp(force, "rows") == 0 && p.rowsS > 0) {
             p.path = mhc::Path::kRows;
+        } else if (std::strcmp(force, "strip") == 0 && p.stripP > 0) {
+            p.path = mhc::Path::kStrip;
         }
     }
     if (const char *launch = std::getenv("MHCPRE_LAUNCH")) {
@@ -467,9 +481,10 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
             done = true;
         }
     }
-    if (!done && p.fusedP > 0 && p.path != mhc::Path::kSplit) {
-        // Teams of fusedP workgroups must be co-resident; a device too small
-        // for one team runs the split path instead.
+    if (!done && p.fusedP > 0 && (p.path == mhc::Path::kFused || p.path == mhc::Path::kStrip)) {
+        // The fused path, or the strip path's fallback on a device too small
+        // for a strip team.  Teams of fusedP workgroups must be co-resident; a
+        // device too small for one team runs the split path instead.
         const int coresident = mhc::fused_max_coresident(p, shape.cus);
         if (coresident >= p.fusedP) {
             mhc::Plan lp = p;

@@ -1,4 +1,4 @@
-// Row-block kernels for gfx950 (rows path: n = 6 and n = 8, K % 128 == 0).
+// Row-block kernels for gfx950 (rows path, K % 128 == 0: n = 6 and 8, and small n = 4 batches).
 //
 // Why x is read twice here.  For n = 8 the B operand of the mixing GEMM
 // (gamma * phi split into bf16 hi + lo, 2M = 160 columns) takes 320 bytes per
@@ -879,6 +879,9 @@ int rows_stage_ksteps() { return kStageKs; }
 hipError_t launch_rows(const Plan &p, void *workspace, int nXcd, int nCu, hipStream_t stream)
 {
     switch (p.n) {
+    case 4:
+        return p.isBf16 ? launch_rows_t<4, true>(p, workspace, nXcd, nCu, stream)
+                        : launch_rows_t<4, false>(p, workspace, nXcd, nCu, stream);
     case 6:
         return p.isBf16 ? launch_rows_t<6, true>(p, workspace, nXcd, nCu, stream)
                         : launch_rows_t<6, false>(p, workspace, nXcd, nCu, stream);

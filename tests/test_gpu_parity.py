@@ -84,7 +84,8 @@ def check(out, ref, x_bits, is_bf16, orc):
 
 
 @pytest.mark.parametrize("cfg,force", [(1, None), (2, None), (4, None), (1, "split"),
-                                       (2, "split"), (1, "fused"), (2, "fused")])
+                                       (2, "split"), (1, "fused"), (2, "fused"), (1, "rows"),
+                                       (2, "rows"), (1, "strip")])
 def test_config_full_parity(pkg, orc, device, cfg, force):
     case = CONFIGS[cfg]
     _say(f"[parity] config {cfg} force={force}: {case}")
@@ -215,7 +216,7 @@ def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
     bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
     gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
     _say(f"[strip-teams] T={T} D={D} bf16={is_bf16} gamma={has_gamma}")
-    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma, force_path="strip")
     assert out["path"] == "strip"
     ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
     check(out, ref, x, is_bf16, orc)

@@ -158,7 +158,7 @@ def test_launch_rejects_bad_workspace_before_any_device_work(pkg, lib):
     assert lib.mhcPre(ctypes.c_void_p(FAKE), ws, None, None) == 1
     name = ctypes.c_char_p()
     assert lib.mhcPreExecutorPath(exe, ctypes.byref(name)) == 0
-    assert name.value in (b"split", b"fused", b"strip")
+    assert name.value in (b"split", b"fused", b"strip", b"rows")
     assert lib.mhcPreExecutorDestroy(exe) == 0
     assert lib.mhcPreExecutorDestroy(None) == 1
 
@@ -214,9 +214,12 @@ def _path(pkg, lib, d, env=None):
 
 
 @pytest.mark.parametrize("n,D,S,want", [
-    (4, 7168, 64, "strip"),    # D % 256 == 0, D / 256 <= 31
-    (4, 64, 64, "fused"),      # n = 4, D % 64 == 0, not a strip shape
+    (4, 7168, 4096, "strip"),  # D % 256 == 0, D / 256 <= 31
+    (4, 64, 4096, "fused"),    # n = 4, D % 64 == 0, not a strip shape
     (4, 48, 64, "split"),      # n = 4, D % 64 != 0
+    (4, 7168, 128, "rows"),    # small n = 4 batch (T <= 128), K % 128 == 0
+    (4, 256, 128, "rows"),
+    (4, 7168, 129, "strip"),
     (8, 7168, 64, "rows"),     # n = 8, K % 128 == 0
     (8, 8192, 5472, "rows"),
     (6, 1024, 16, "rows"),     # K = 6144
@@ -231,5 +234,6 @@ def test_forced_paths(pkg, lib):
     d = _descs(pkg, S=64, n=8, D=1024)
     assert _path(pkg, lib, d, env="split") == "split"
     assert _path(pkg, lib, d, env="rows") == "rows"
+    assert _path(pkg, lib, _descs(pkg, S=64, n=4, D=7168), env="strip") == "strip"
     # A path the shape cannot take is ignored.
     assert _path(pkg, lib, _descs(pkg, S=16, n=6, D=48), env="rows") == "split"
