@@ -251,11 +251,12 @@ def test_zero_and_constant_rows(pkg, orc, device):
     assert (ulp_distance(out["h_in"][:16], np.zeros_like(out["h_in"][:16])) == 0).all()
 
 
-def test_determinism(pkg, device):
+@pytest.mark.parametrize("cfg", [2, 4])
+def test_determinism(pkg, device, cfg):
     """Two launches give bitwise-identical outputs (fixed-order reductions, no atomics)."""
     import torch
 
-    case = CONFIGS[2]
+    case = CONFIGS[cfg]
     x, phi, alpha, bias, gamma = make_case(case)
     xt, pt, at, bt, gt = to_device(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma)
     op = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True)
@@ -270,8 +271,11 @@ def test_determinism(pkg, device):
     op.close()
 
 
-@pytest.mark.parametrize("force,expect", [(None, "strip"), ("fused", "fused")])
-def test_shared_workspace_back_to_back(pkg, orc, device, force, expect):
+@pytest.mark.parametrize("force,expect,n,T,D", [(None, "strip", 4, 400, 7168),
+                                               ("fused", "fused", 4, 400, 7168),
+                                               (None, "rows", 8, 300, 2048),
+                                               (None, "rows", 8, 48, 2048)])
+def test_shared_workspace_back_to_back(pkg, orc, device, force, expect, n, T, D):
     """Two executors with different inputs launched back to back on ONE
     workspace: nothing from the first launch (exchange records, published
     hPre) may leak into the second."""
@@ -279,7 +283,6 @@ def test_shared_workspace_back_to_back(pkg, orc, device, force, expect):
 
     import torch
 
-    T, n, D = 400, 4, 7168
     K, M = n * D, n * n + 2 * n
     ops, refs, xs = [], [], []
     ws = None
