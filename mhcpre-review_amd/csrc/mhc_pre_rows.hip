@@ -858,8 +858,10 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, int nCu, hipS
     e.normEps = p.normEps;
     e.hcEps = p.hcEps;
     e.invFlatDim = p.invFlatDim;
-    // Many K-ranges (small batches): more threads share each row's sums.
-    if (p.rowsS > 32) {
+    // Many K-ranges: more threads share each row's sums once a 256-thread
+    // group would add more than 8 partials per column.
+    constexpr int kCols = C::M + 1;
+    if ((p.rowsS + 256 / kCols - 1) / (256 / kCols) > 8) {
         hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16, 1024, 1>), dim3((unsigned)p.T), dim3(1024),
                            0, stream, e);
     } else {
