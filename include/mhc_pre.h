@@ -119,10 +119,10 @@ MHC_API int mhcPreGetWorkspaceSizeWithHPre(const mhcTensor *x, const mhcTensor *
  * the operator on `stream` (NULL = the null stream) and returns without
  * waiting.  The workspace must hold at least the bytes phase 1 returned.
  *
- * The fused kernel's workgroups wait on each other (bounded), so its grid is
- * sized to what the device holds at once.  By default it is a plain launch:
- * every workgroup is resident unless another kernel occupies the device at
- * the same time, in which case a wait can expire and
+ * The strip and fused kernels' workgroups wait on each other (bounded), so
+ * their grids are sized to what the device holds at once.  By default it is a
+ * plain launch: every workgroup is resident unless another kernel occupies the
+ * device at the same time, in which case a wait can expire and
  * mhcPreQueryDeviceStatus reports MHC_STATUS_DEVICE_TIMEOUT (no hang).  With
  * the environment variable MHCPRE_LAUNCH=cooperative at phase 1 the executor
  * uses a cooperative launch, which guarantees co-residency next to concurrent

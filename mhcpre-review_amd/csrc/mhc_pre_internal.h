@@ -38,10 +38,10 @@ struct Plan {
     bool isBf16 = true;
     bool hasGamma = false;
     bool hasHPre = false;
-    // Fused path launch.  By default a plain launch of a grid sized to the
-    // device's co-residency limit: every workgroup is resident as long as no
-    // other kernel occupies the device, and the kernel's bounded waits turn
-    // any other case into a reported timeout rather than a hang.
+    // Strip and fused path launch.  By default a plain launch of a grid sized
+    // to the device's co-residency limit: every workgroup is resident as long
+    // as no other kernel occupies the device, and the kernels' bounded waits
+    // turn any other case into a reported timeout rather than a hang.
     // MHCPRE_LAUNCH=cooperative selects a cooperative launch, which
     // guarantees co-residency next to concurrent work at the cost of a
     // slower dispatch (about 20 us per launch on MI355X).

@@ -934,9 +934,17 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
     a.invFlatDim = p.invFlatDim;
     a.epoch = epoch;
     a.spinLimit = 1u << 20;  // about a second of polling per wait
-    hipLaunchKernelGGL((strip_kernel<N, kBf16>), dim3((unsigned)p.stripGrid), dim3(kWaves * 64), 0,
-                       stream, a);
-    return hipGetLastError();
+    if (!p.fusedCooperative) {
+        hipLaunchKernelGGL((strip_kernel<N, kBf16>), dim3((unsigned)p.stripGrid), dim3(kWaves * 64), 0,
+                           stream, a);
+        return hipGetLastError();
+    }
+    // Cooperative launch (MHCPRE_LAUNCH=cooperative): co-residency of the
+    // whole grid is guaranteed even next to concurrent work.
+    void *args[] = {&a};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&strip_kernel<N, kBf16>),
+                                      dim3((unsigned)p.stripGrid), dim3(kWaves * 64), args, 0,
+                                      stream);
 }
 
 }  // namespace

@@ -95,16 +95,17 @@ def test_config_full_parity(pkg, orc, device, cfg, force):
     check(out, ref, x, case.is_bf16, orc)
 
 
-def test_cooperative_launch_matches(pkg, orc, device):
+@pytest.mark.parametrize("force", ["fused", "strip"])
+def test_cooperative_launch_matches(pkg, orc, device, force):
     """The cooperative launch mode (MHCPRE_LAUNCH=cooperative) runs the same
-    fused kernel: bit-identical outputs to the default launch, and parity."""
+    kernel: bit-identical outputs to the default launch, and parity."""
     case = CONFIGS[2]
-    _say(f"[parity] config 2 cooperative launch: {case}")
+    _say(f"[parity] config 2 cooperative launch ({force}): {case}")
     x, phi, alpha, bias, gamma = make_case(case)
     coop = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, launch="cooperative",
-                   force_path="fused")
-    plain = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, force_path="fused")
-    assert coop["path"] == plain["path"] == "fused"
+                   force_path=force)
+    plain = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, force_path=force)
+    assert coop["path"] == plain["path"] == force
     for k in ("h_in", "h_post", "h_res", "h_pre"):
         assert np.array_equal(coop[k], plain[k]), k
     ref = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
