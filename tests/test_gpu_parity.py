@@ -327,6 +327,9 @@ def test_shared_workspace_back_to_back(pkg, orc, device, force, expect, n, T, D)
     (64, 6, 1024, True, True),      # small-batch GEMM (T <= 64): B built from phi in registers
     (40, 8, 4096, True, True),      # small-batch GEMM, rows past T in the last 16-row block
     (2, 6, 2048, False, False),     # small-batch GEMM, fp16, two rows
+    (20000, 8, 64, True, True),     # 79 row blocks, K = 512: one stage per K-range
+    (64, 8, 16384, True, True),     # small-batch GEMM, K = 131072: 512 K-ranges
+    (600, 8, 16384, False, True),   # K = 131072 on the block GEMM, fp16
 ])
 def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     """Row-block path (n = 6, 8): ragged row blocks, several K-ranges, fp16 and
