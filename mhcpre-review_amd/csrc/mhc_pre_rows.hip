@@ -514,6 +514,8 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
         gm[kk][0] = gsrc[0];
         gm[kk][1] = gsrc[1];
     }
+    // Every load is issued before any use: one memory round trip.
+    __builtin_amdgcn_sched_barrier(0);
 
     f32x4_t acc[RB][NA];
     f32x4_t gram[RB];
