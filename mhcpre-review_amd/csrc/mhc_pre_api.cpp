@@ -498,7 +498,7 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
     }
     if (!done && p.path == mhc::Path::kRows) {
         executor->lastEpoch.store(next_epoch(), std::memory_order_relaxed);
-        err = mhc::launch_rows(p, workspace, shape.xcds, shape.cus, stream);
+        err = mhc::launch_rows(p, workspace, shape.xcds, stream);
         done = true;
     }
     if (!done) {

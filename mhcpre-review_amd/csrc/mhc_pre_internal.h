@@ -111,9 +111,9 @@ hipError_t launch_fused(const Plan &plan, void *workspace, uint32_t epoch, hipSt
 
 hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
 
-// Rows path (mhc_pre_rows.hip); nXcd, nCu: XCDs and CUs of the device
-// (work placement and grid size only).
-hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, int nCu, hipStream_t stream);
+// Rows path (mhc_pre_rows.hip); nXcd: XCDs of the device (work placement
+// only).
+hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, hipStream_t stream);
 // Rows per work item and k-steps per stage of the rows-path GEMM.
 int rows_block_rows();
 int rows_stage_ksteps();

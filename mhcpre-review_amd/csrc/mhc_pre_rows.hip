@@ -795,9 +795,8 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
 }
 
 template <int N, bool kBf16>
-hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, int nCu, hipStream_t stream)
+hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t stream)
 {
-    (void)nCu;
     char *ws = static_cast<char *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(ws);
     u32x4_t *bfrag = reinterpret_cast<u32x4_t *>(ws + p.wsRowsB);
@@ -880,18 +879,18 @@ int rows_small_rows() { return kSmallRows; }
 int rows_small_ksteps() { return kSmallWaves * kSmallKs; }
 int rows_stage_ksteps() { return kStageKs; }
 
-hipError_t launch_rows(const Plan &p, void *workspace, int nXcd, int nCu, hipStream_t stream)
+hipError_t launch_rows(const Plan &p, void *workspace, int nXcd, hipStream_t stream)
 {
     switch (p.n) {
     case 4:
-        return p.isBf16 ? launch_rows_t<4, true>(p, workspace, nXcd, nCu, stream)
-                        : launch_rows_t<4, false>(p, workspace, nXcd, nCu, stream);
+        return p.isBf16 ? launch_rows_t<4, true>(p, workspace, nXcd, stream)
+                        : launch_rows_t<4, false>(p, workspace, nXcd, stream);
     case 6:
-        return p.isBf16 ? launch_rows_t<6, true>(p, workspace, nXcd, nCu, stream)
-                        : launch_rows_t<6, false>(p, workspace, nXcd, nCu, stream);
+        return p.isBf16 ? launch_rows_t<6, true>(p, workspace, nXcd, stream)
+                        : launch_rows_t<6, false>(p, workspace, nXcd, stream);
     case 8:
-        return p.isBf16 ? launch_rows_t<8, true>(p, workspace, nXcd, nCu, stream)
-                        : launch_rows_t<8, false>(p, workspace, nXcd, nCu, stream);
+        return p.isBf16 ? launch_rows_t<8, true>(p, workspace, nXcd, stream)
+                        : launch_rows_t<8, false>(p, workspace, nXcd, stream);
     default:
         return hipErrorNotSupported;
     }
