@@ -263,8 +263,8 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     if (n == 4 && (D % 256) == 0 && D / 256 <= mhc::strip_max_slices() && T < (int64_t{1} << 24)) {
         p.stripP = static_cast<int>(D / 256);
     }
-    // Rows path (n = 6, 8): 256-row blocks x S K-ranges of contiguous
-    // 4-k-step stages (the last range may be shorter).  S balances whole waves of 256
+    // Rows path (any n, K % 128 == 0): rows_block_rows()-row blocks x S
+    // K-ranges of contiguous stages (the last range may be shorter).  S balances whole waves of 256
     // workgroups (one per CU of an MI355X; S only affects speed) against the
     // partial traffic: cost ~ rounds * (x bytes of one item) + partial bytes
     // written and read.  32-bit buffer offsets bound K and the B bytes.

@@ -73,8 +73,9 @@ struct Plan {
     int stripTeamsPerXcd = 0;
     int stripGrid = 0;
 
-    // Rows path (n = 6, 8; K % 128 == 0): rowsS K-ranges (contiguous runs
-    // of 4-k-step stages) over rowsBlocks blocks of 256 rows.
+    // Rows path (K % 128 == 0): rowsS K-ranges (contiguous runs of
+    // rows_stage_ksteps()-k-step stages) over rowsBlocks blocks of
+    // rows_block_rows() rows.
     int rowsS = 0;
     int rowsBlocks = 0;
     // Small batches (T <= rows_small_rows()): one GEMM workgroup per K-range
