@@ -50,6 +50,37 @@ __device__ __forceinline__ uint32_t f32_to_x(float f)
     return kBf16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f);
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to a packed pair (a in the low half), round-half-even: one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32, where two scalar conversions cost two
+// conversions, a shift and an or.
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
+__device__ __forceinline__ uint32_t pack2_f16(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+}
+
+template <bool kBf16>
+__device__ __forceinline__ uint32_t pack2_x(float a, float b)
+{
+    return kBf16 ? pack2_bf16(a, b) : pack2_f16(a, b);
+}
+
+// Packed bf16 hi + lo of two floats: hi = bf16(v), lo = bf16(v - hi), both
+// round-half-even (v - hi is exact in fp32).
+__device__ __forceinline__ void split2_bf16(float a, float b, uint32_t &hi, uint32_t &lo)
+{
+    hi = pack2_bf16(a, b);
+    lo = pack2_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
+}
+
 // Unpack 8 16-bit values held in a u32x4 (element e in half e&1 of word e>>1).
 template <bool kBf16>
 __device__ __forceinline__ void unpack8(const u32x4_t &v, float (&f)[8])
@@ -66,7 +97,7 @@ __device__ __forceinline__ u32x4_t pack8_bf16(const float (&f)[8])
     u32x4_t r;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        r[w] = f32_to_bf16_bits(f[2 * w]) | (f32_to_bf16_bits(f[2 * w + 1]) << 16);
+        r[w] = pack2_bf16(f[2 * w], f[2 * w + 1]);
     }
     return r;
 }
@@ -127,14 +158,13 @@ __device__ __forceinline__ f32x4_t mfma16(const u32x4_t &a, const u32x4_t &b, co
 // fp16 x -> exact bf16 pair: x = hi + lo (an fp16 significand has 11 bits).
 __device__ __forceinline__ void split_f16_to_bf16(const float (&f)[8], u32x4_t &hi, u32x4_t &lo)
 {
-    float h[8], l[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        h[e] = bf16_bits_to_f32(f32_to_bf16_bits(f[e]));
-        l[e] = f[e] - h[e];
+    for (int w = 0; w < 4; ++w) {
+        uint32_t h, l;
+        split2_bf16(f[2 * w], f[2 * w + 1], h, l);
+        hi[w] = h;
+        lo[w] = l;
     }
-    hi = pack8_bf16(h);
-    lo = pack8_bf16(l);
 }
 
 // Sigmoid in the reference vector order (code/op_kernel/mhc_pre.cpp:542-555):

@@ -669,7 +669,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
                 u32x4_t o;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
-                    o[w] = f32_to_x<kBf16>(hv[2 * w]) | (f32_to_x<kBf16>(hv[2 * w + 1]) << 16);
+                    o[w] = pack2_x<kBf16>(hv[2 * w], hv[2 * w + 1]);
                 }
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, o), hrs,

@@ -262,7 +262,7 @@ __global__ __launch_bounds__(256) void epilogue_hin_kernel(
         u32x4_t o;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            o[w] = f32_to_x<kBf16>(acc[2 * w]) | (f32_to_x<kBf16>(acc[2 * w + 1]) << 16);
+            o[w] = pack2_x<kBf16>(acc[2 * w], acc[2 * w + 1]);
         }
         *reinterpret_cast<u32x4_t *>(out + d8 * 8) = o;
     }

@@ -188,15 +188,17 @@ __global__ __launch_bounds__(256) void rows_prep_b_kernel(const float *__restric
             b[e] = b[e] * g[e];
         }
     }
-    float hi[8], lo[8];
+    u32x4_t hi, lo;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        hi[e] = bf16_bits_to_f32(f32_to_bf16_bits(b[e]));
-        lo[e] = b[e] - hi[e];
+    for (int w = 0; w < 4; ++w) {
+        uint32_t h, l;
+        split2_bf16(b[2 * w], b[2 * w + 1], h, l);
+        hi[w] = h;
+        lo[w] = l;
     }
     u32x4_t *dst = bfrag + ks * C::NT * kWave;
-    dst[thi * kWave + lhi] = pack8_bf16(hi);
-    dst[tlo * kWave + llo] = pack8_bf16(lo);
+    dst[thi * kWave + lhi] = hi;
+    dst[tlo * kWave + llo] = lo;
 }
 
 // ---------------------------------------------------------------------------
@@ -541,18 +543,22 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
         }
 #pragma unroll
         for (int ta = 0; ta < NA; ++ta) {
-            float hi[8], lo[8];
+            float b[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                float b = ph[kk][ta][e >> 2][e & 3];
+                b[e] = ph[kk][ta][e >> 2][e & 3];
                 if (hasGamma) {
-                    b = b * gm[kk][e >> 2][e & 3];
+                    b[e] = b[e] * gm[kk][e >> 2][e & 3];
                 }
-                hi[e] = bf16_bits_to_f32(f32_to_bf16_bits(b));
-                lo[e] = b - hi[e];
             }
-            const u32x4_t bh = pack8_bf16(hi);
-            const u32x4_t bl = pack8_bf16(lo);
+            u32x4_t bh, bl;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t h, l;
+                split2_bf16(b[2 * w], b[2 * w + 1], h, l);
+                bh[w] = h;
+                bl[w] = l;
+            }
             if (ta < Q) {
 #pragma unroll
                 for (int r = 0; r < RB; ++r) {
@@ -783,7 +789,7 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
             u32x4_t out;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                out[w] = f32_to_x<kBf16>(acc[2 * w]) | (f32_to_x<kBf16>(acc[2 * w + 1]) << 16);
+                out[w] = pack2_x<kBf16>(acc[2 * w], acc[2 * w + 1]);
             }
             if (d8 < DO) {
                 __builtin_amdgcn_raw_buffer_store_b128(

@@ -709,7 +709,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    hout[h][q] = f32_to_x<kBf16>(hv[2 * q]) | (f32_to_x<kBf16>(hv[2 * q + 1]) << 16);
+                    hout[h][q] = pack2_x<kBf16>(hv[2 * q], hv[2 * q + 1]);
                 }
             }
             //    Poll for the hIn of the next step (own tile jh + 1; the
