@@ -67,7 +67,8 @@ typedef struct mhcPreExecutor mhcPreExecutor;
 #define MHC_STATUS_SUCCESS 0
 #define MHC_STATUS_NULL_ARGUMENT 1        /* a required pointer is NULL */
 #define MHC_STATUS_INVALID_SHAPE 2        /* rank / dims / element counts inconsistent */
-#define MHC_STATUS_UNSUPPORTED_SHAPE 3    /* n not in {4,6,8}, D % 16, n*D % 8, M > 80 */
+#define MHC_STATUS_UNSUPPORTED_SHAPE 3    /* n not in {4,6,8}, D % 16, n*D % 8, M > 80,
+                                             B*S >= 2^28 rows, D > 2^24 */
 #define MHC_STATUS_INVALID_DTYPE 4        /* x not fp16/bf16, fp32 tensors not fp32, hIn != x */
 #define MHC_STATUS_WORKSPACE_TOO_SMALL 5  /* workspace NULL or smaller than phase 1 asked */
 #define MHC_STATUS_HIP_ERROR 6            /* a HIP runtime call failed */

@@ -33,11 +33,23 @@ struct mhcPreExecutor {
 
 namespace {
 
+// Largest row count (B*S) and per-stream width D a launch plan accepts: the
+// split path's GEMM grid has T/16 workgroups of 256 work-items in its x
+// dimension, which must stay below 2^32; D <= 2^24 keeps K = n*D and every
+// byte offset formed from T and K far inside 64 bits.
+constexpr int64_t kMaxRows = int64_t{1} << 28;
+constexpr int64_t kMaxWidth = int64_t{1} << 24;
+
+// Product of the dims, or -1 if it does not fit in 62 bits (a tensor that
+// large fits no device); 0 if a dim is 0.  Negative dims give a negative or
+// meaningless product, which every caller rejects with dims_positive.
 int64_t numel(const mhcTensor &t)
 {
     int64_t n = 1;
     for (int i = 0; i < t.ndim; ++i) {
-        n *= t.dims[i];
+        if (__builtin_mul_overflow(n, t.dims[i], &n) || n > (int64_t{1} << 62)) {
+            return -1;
+        }
     }
     return n;
 }
@@ -147,12 +159,17 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         if (x->dims[i] <= 0) {
             return MHC_STATUS_INVALID_SHAPE;
         }
-        T *= x->dims[i];
+        if (__builtin_mul_overflow(T, x->dims[i], &T) || T >= kMaxRows) {
+            return MHC_STATUS_UNSUPPORTED_SHAPE;
+        }
     }
     const int64_t n64 = x->dims[x->ndim - 2];
     const int64_t D = x->dims[x->ndim - 1];
     if (D <= 0) {
         return MHC_STATUS_INVALID_SHAPE;
+    }
+    if (D > kMaxWidth) {
+        return MHC_STATUS_UNSUPPORTED_SHAPE;
     }
     // Supported stream counts and alignments (code/op_host/mhc_pre.cpp:76-79,126-128).
     if (n64 != 4 && n64 != 6 && n64 != 8) {
@@ -282,6 +299,9 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             if (S > 1 && (NS + S - 2) / (S - 1) == perItem) {
                 continue;  // same stages per item with fewer ranges; this
                            // also keeps every range non-empty
+            }
+            if ((blocks * S + 255) * mhc::rows_gemm_threads() >= (int64_t{1} << 32)) {
+                break;  // the GEMM grid's work-items must stay below 2^32
             }
             const int64_t rounds = (blocks * S + kSlotsPerRound - 1) / kSlotsPerRound;
             const double cost = static_cast<double>(rounds) * static_cast<double>(std::min(T, blockRows)) *

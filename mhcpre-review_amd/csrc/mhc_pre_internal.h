@@ -115,9 +115,11 @@ hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t epoch, hipSt
 // Rows path (mhc_pre_rows.hip); nXcd: XCDs of the device (work placement
 // only).
 hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, hipStream_t stream);
-// Rows per work item and k-steps per stage of the rows-path GEMM.
+// Rows per work item, k-steps per stage and work-items per workgroup of the
+// rows-path GEMM.
 int rows_block_rows();
 int rows_stage_ksteps();
+int rows_gemm_threads();
 // Largest batch of the small-batch GEMM and k-steps per workgroup there.
 int rows_small_rows();
 int rows_small_ksteps();
@@ -134,6 +136,11 @@ int strip_max_slices();
 // workgroups per team are left over after the slices (1, 2 or 4; the ring
 // size depends on it).
 int strip_reducers(int available);
+
+// Rows per launch of the one-workgroup-per-row epilogue kernels (rows and
+// split paths): a grid's work-items must stay below 2^32, so larger batches
+// take several launches.
+constexpr int64_t kEpilogueRowsPerLaunch = int64_t{1} << 20;
 
 // Largest number of fused-path workgroups that can be co-resident on a device
 // with numCUs compute units, or -1 if the plan has no fused kernel.

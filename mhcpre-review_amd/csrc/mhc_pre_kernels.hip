@@ -19,6 +19,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 namespace mhc {
 namespace {
 
@@ -191,14 +193,14 @@ __global__ __launch_bounds__(256) void gemm_partial_kernel(const uint16_t *__res
 template <int N, bool kBf16>
 __global__ __launch_bounds__(256) void epilogue_hin_kernel(
     const uint16_t *__restrict__ x, const float *__restrict__ partial, int S, int64_t T,
-    int64_t D, const float *__restrict__ alpha, const float *__restrict__ bias, float normEps,
-    float hcEps, float invFlatDim, uint16_t *__restrict__ hIn, float *__restrict__ hPost,
-    float *__restrict__ hRes, float *__restrict__ hPre)
+    int64_t D, int64_t row0, const float *__restrict__ alpha, const float *__restrict__ bias,
+    float normEps, float hcEps, float invFlatDim, uint16_t *__restrict__ hIn,
+    float *__restrict__ hPost, float *__restrict__ hRes, float *__restrict__ hPre)
 {
     constexpr int M = Shape<N>::M;
     __shared__ float smix[M + 1];
     __shared__ float spre[N];
-    const int64_t row = blockIdx.x;
+    const int64_t row = row0 + blockIdx.x;  // row0: first row of this launch
     const int tid = threadIdx.x;
 
     if (tid <= M) {
@@ -292,12 +294,20 @@ hipError_t launch_split_t(const Plan &p, void *workspace, hipStream_t stream)
     if (err != hipSuccess) {
         return err;
     }
-    hipLaunchKernelGGL((epilogue_hin_kernel<N, kBf16>), dim3((unsigned)p.T), dim3(256), 0, stream,
-                       static_cast<const uint16_t *>(p.x), partial, p.splitS, p.T, p.D, p.alpha,
-                       p.bias, p.normEps, p.hcEps, p.invFlatDim,
-                       static_cast<uint16_t *>(p.hIn), p.hPost, p.hRes,
-                       p.hasHPre ? p.hPre : nullptr);
-    return hipGetLastError();
+    // One workgroup per row, kEpilogueRowsPerLaunch rows per launch.
+    for (int64_t r0 = 0; r0 < p.T; r0 += kEpilogueRowsPerLaunch) {
+        const dim3 grid((unsigned)std::min<int64_t>(kEpilogueRowsPerLaunch, p.T - r0));
+        hipLaunchKernelGGL((epilogue_hin_kernel<N, kBf16>), grid, dim3(256), 0, stream,
+                           static_cast<const uint16_t *>(p.x), partial, p.splitS, p.T, p.D, r0,
+                           p.alpha, p.bias, p.normEps, p.hcEps, p.invFlatDim,
+                           static_cast<uint16_t *>(p.hIn), p.hPost, p.hRes,
+                           p.hasHPre ? p.hPre : nullptr);
+        err = hipGetLastError();
+        if (err != hipSuccess) {
+            return err;
+        }
+    }
+    return hipSuccess;
 }
 
 }  // namespace

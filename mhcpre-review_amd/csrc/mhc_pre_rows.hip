@@ -648,6 +648,7 @@ struct RowsEpiArgs {
     float *hPre;
     int64_t T;
     int64_t D;
+    int64_t row0;  // row of workgroup 0 (launches of kEpilogueRowsPerLaunch rows)
     int S;
     float normEps;
     float hcEps;
@@ -664,7 +665,7 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
     __shared__ float smix[COLS];
     __shared__ float spre[N];
 
-    const int64_t row = blockIdx.x;
+    const int64_t row = a.row0 + blockIdx.x;
     const int tid = threadIdx.x;
     const int64_t DO = a.D / 8;  // column octets
     const int Di2 = (int)(a.D * 2);
@@ -868,19 +869,27 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
     // Many K-ranges: more threads share each row's sums once a 256-thread
     // group would add more than 8 partials per column.
     constexpr int kCols = C::M + 1;
-    if ((p.rowsS + 256 / kCols - 1) / (256 / kCols) > 8) {
-        hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16, 1024, 1>), dim3((unsigned)p.T), dim3(1024),
-                           0, stream, e);
-    } else {
-        hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16, 256, 4>), dim3((unsigned)p.T), dim3(256),
-                           0, stream, e);
+    const bool wide = (p.rowsS + 256 / kCols - 1) / (256 / kCols) > 8;
+    for (int64_t r0 = 0; r0 < p.T; r0 += kEpilogueRowsPerLaunch) {
+        e.row0 = r0;
+        const dim3 grid((unsigned)std::min<int64_t>(kEpilogueRowsPerLaunch, p.T - r0));
+        if (wide) {
+            hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16, 1024, 1>), grid, dim3(1024), 0, stream, e);
+        } else {
+            hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16, 256, 4>), grid, dim3(256), 0, stream, e);
+        }
+        err = hipGetLastError();
+        if (err != hipSuccess) {
+            return err;
+        }
     }
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 }  // namespace
 
 int rows_block_rows() { return kRowBlock; }
+int rows_gemm_threads() { return kRW * 64; }
 int rows_small_rows() { return kSmallRows; }
 int rows_small_ksteps() { return kSmallWaves * kSmallKs; }
 int rows_stage_ksteps() { return kStageKs; }

@@ -118,6 +118,26 @@ def test_validation_status_codes(pkg, lib, over, want):
     assert st == code(pkg, want), (over, st)
 
 
+def test_size_limits_and_overflowing_dims(pkg, lib):
+    """Row counts from 2^28 and widths above 2^24 are unsupported (the split
+    GEMM's grid and 64-bit byte offsets); dims whose products overflow are
+    rejected, not wrapped."""
+    ok = _descs(pkg, B=(1 << 28) - 1, S=1, n=4, D=16)
+    assert _call(pkg, lib, ok)[0] == code(pkg, "MHC_STATUS_SUCCESS")
+    ok8 = _descs(pkg, B=(1 << 28) - 1, S=1, n=8, D=16)
+    assert _call(pkg, lib, ok8)[0] == code(pkg, "MHC_STATUS_SUCCESS")
+    big = _descs(pkg, B=1 << 27, S=2, n=4, D=16)
+    assert _call(pkg, lib, big)[0] == code(pkg, "MHC_STATUS_UNSUPPORTED_SHAPE")
+    wrap = _descs(pkg, B=1 << 62, S=4, n=4, D=16)
+    assert _call(pkg, lib, wrap)[0] == code(pkg, "MHC_STATUS_UNSUPPORTED_SHAPE")
+    wide = _descs(pkg, B=1, S=1, n=4, D=(1 << 24) + 16)
+    assert _call(pkg, lib, wide)[0] == code(pkg, "MHC_STATUS_UNSUPPORTED_SHAPE")
+    # A phi whose element count wraps modulo 2^64 onto K*M = 6144 exactly.
+    d = _descs(pkg)
+    d["phi"] = (FAKE, pkg.MHC_DTYPE_FLOAT, [4, (1 << 62) + 1536])
+    assert _call(pkg, lib, d)[0] == code(pkg, "MHC_STATUS_INVALID_SHAPE")
+
+
 def test_null_descriptors_and_outputs(pkg, lib):
     mk = lambda v: ctypes.byref(pkg.make_tensor(*v))
     d = _descs(pkg)
