@@ -72,7 +72,8 @@ typedef struct mhcPreExecutor mhcPreExecutor;
 #define MHC_STATUS_INVALID_DTYPE 4        /* x not fp16/bf16, fp32 tensors not fp32, hIn != x */
 #define MHC_STATUS_WORKSPACE_TOO_SMALL 5  /* workspace NULL or smaller than phase 1 asked */
 #define MHC_STATUS_HIP_ERROR 6            /* a HIP runtime call failed */
-#define MHC_STATUS_DEVICE_MISMATCH 7      /* launched on a device the executor cannot run on */
+#define MHC_STATUS_DEVICE_MISMATCH 7      /* phase 2 called with another device current than
+                                             the one holding x at phase 1 */
 #define MHC_STATUS_DEVICE_TIMEOUT 8       /* a kernel's bounded inter-workgroup wait expired */
 #define MHC_STATUS_MISALIGNED 9           /* x, hIn, phi, gamma not 16-byte aligned; others not 4 */
 
@@ -118,7 +119,10 @@ MHC_API int mhcPreGetWorkspaceSizeWithHPre(const mhcTensor *x, const mhcTensor *
 /*
  * Phase 2.  Replaces aclnnMhcPre (cloud_runner/runner.cpp:459,472): enqueues
  * the operator on `stream` (NULL = the null stream) and returns without
- * waiting.  The workspace must hold at least the bytes phase 1 returned.
+ * waiting.  The workspace must hold at least the bytes phase 1 returned.  The
+ * device holding the tensors must be the current device
+ * (MHC_STATUS_DEVICE_MISMATCH otherwise), as aclnn launches run on the
+ * context's device.
  *
  * The strip and fused kernels' workgroups wait on each other (bounded), so
  * their grids are sized to what the device holds at once.  By default it is a

@@ -207,9 +207,14 @@ class MhcPreOp:
         return name.value.decode()
 
     def launch(self, stream=None) -> None:
-        st = self.lib.mhcPre(ctypes.c_void_p(self.workspace.data_ptr()),
-                             ctypes.c_uint64(self.workspace_size), self.executor,
-                             ctypes.c_void_p(_stream_handle(stream)))
+        import torch
+
+        # The library launches on the current device, which must hold the
+        # tensors; the default stream is that device's current stream.
+        with torch.cuda.device(self.workspace.device):
+            st = self.lib.mhcPre(ctypes.c_void_p(self.workspace.data_ptr()),
+                                 ctypes.c_uint64(self.workspace_size), self.executor,
+                                 ctypes.c_void_p(_stream_handle(stream)))
         if st != 0:
             raise MhcPreError("mhcPre", st)
 

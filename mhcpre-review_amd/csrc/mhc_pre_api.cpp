@@ -25,7 +25,9 @@
 
 struct mhcPreExecutor {
     mhc::Plan plan;
-    int device = -1;  // device the executor was planned on (-1: none visible at plan time)
+    // Device that holds x (-1: the runtime could not tell, e.g. no device is
+    // visible at phase 1); launches must have it current.
+    int device = -1;
     // Epoch of this executor's latest launch; the device status word only
     // reports a timeout written under it.
     std::atomic<uint32_t> lastEpoch{0};
@@ -104,6 +106,18 @@ bool device_shape(int &device, DeviceShape &out)
     }
     out = cache[device];
     return true;
+}
+
+// Device that holds the device memory at `p`, or -1 when the runtime cannot
+// tell (host memory, an address no allocation covers, no device visible).
+int device_of(const void *p)
+{
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
+    }
+    return attr.type == hipMemoryTypeDevice ? attr.device : -1;
 }
 
 // Launch epochs: process-wide, strictly increasing from a start that differs
@@ -419,12 +433,7 @@ int get_workspace(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alp
         return MHC_STATUS_HIP_ERROR;
     }
     ex->plan = plan;
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess) {
-        (void)hipGetLastError();
-        dev = -1;
-    }
-    ex->device = dev;
+    ex->device = device_of(plan.x);
     *workspaceSize = plan.wsTotal;
     *executor = ex;
     return MHC_STATUS_SUCCESS;
@@ -466,6 +475,18 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
     }
     if (!aligned(workspace, 256)) {
         return MHC_STATUS_WORKSPACE_TOO_SMALL;
+    }
+    // The kernels run on the current device and address the executor's
+    // tensors directly: it must be the device that holds them.
+    if (executor->device >= 0) {
+        int current = -1;
+        if (hipGetDevice(&current) != hipSuccess) {
+            (void)hipGetLastError();
+            return MHC_STATUS_HIP_ERROR;
+        }
+        if (current != executor->device) {
+            return MHC_STATUS_DEVICE_MISMATCH;
+        }
     }
     hipError_t err = hipSuccess;
     bool done = false;
