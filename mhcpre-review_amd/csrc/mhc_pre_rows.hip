@@ -701,20 +701,42 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         const float *src = a.partial + row * COLS + j;
         const int64_t stride = a.T * COLS;
         float v = 0.f;
-        int sk = sBeg;
-        for (; sk + 8 <= sEnd; sk += 8) {
-            float t[8];
+        if constexpr (kEpiThreads >= 1024) {
+            // Many K-ranges (this variant is taken when a group would have
+            // more than 8 partials): up to 32 are loaded before the first add
+            // (one memory round trip, where a load per add costs one each),
+            // then added in K-range order.  Slots past the group's range
+            // re-read its last partial and are not added.
+            constexpr int kBatch = 32;
+            for (int sk = sBeg; sk < sEnd; sk += kBatch) {
+                float t[kBatch];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                t[i] = src[(int64_t)(sk + i) * stride];
-            }
+                for (int i = 0; i < kBatch; ++i) {
+                    t[i] = src[(int64_t)min(sk + i, sEnd - 1) * stride];
+                }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                v = v + t[i];
+                for (int i = 0; i < kBatch; ++i) {
+                    if (sk + i < sEnd) {
+                        v = v + t[i];
+                    }
+                }
             }
-        }
-        for (; sk < sEnd; ++sk) {
-            v = v + src[(int64_t)sk * stride];
+        } else {
+            int sk = sBeg;
+            for (; sk + 8 <= sEnd; sk += 8) {
+                float t[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    t[i] = src[(int64_t)(sk + i) * stride];
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    v = v + t[i];
+                }
+            }
+            for (; sk < sEnd; ++sk) {
+                v = v + src[(int64_t)sk * stride];
+            }
         }
         red[q][j] = v;
     }
