@@ -668,10 +668,17 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
     const int64_t row = a.row0 + blockIdx.x;
     const int tid = threadIdx.x;
     const int64_t DO = a.D / 8;  // column octets
+    // Part blockIdx.y of gridDim.y writes the hIn octets [oBeg, oEnd) of the
+    // row; every part evaluates the row's sums, part 0 writes hPost, hRes
+    // and hPre.
+    const int64_t partOct = (DO + gridDim.y - 1) / gridDim.y;
+    const int64_t oBeg = min(DO, (int64_t)blockIdx.y * partOct);
+    const int64_t oEnd = min(DO, oBeg + partOct);
+    const bool part0 = blockIdx.y == 0;
     const int Di2 = (int)(a.D * 2);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + row * N * a.D, N * Di2);
     const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.hIn + row * a.D, Di2);
-    const int xLane = tid * 16;
+    const int xLane = (int)(oBeg + tid) * 16;
 
     // bias and alpha for this thread's output column, loaded up front so
     // that their round trip overlaps the others.
@@ -679,8 +686,8 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
     const float alphaJ = tid < N ? a.alpha[0] : (tid < 2 * N ? a.alpha[1] : a.alpha[2]);
 
     // First pass of x loads, issued before the partial sums so that both
-    // round trips overlap.  Octets past D read other streams' data or zeros
-    // (size-bounded resource) and are not stored.
+    // round trips overlap.  Octets past the part read other columns' data or
+    // zeros (size-bounded resource) and are not stored.
     u32x4_t xv[kEpiOct][N];
 #pragma unroll
     for (int o = 0; o < kEpiOct; ++o) {
@@ -758,15 +765,17 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         if (tid < N) {
             const float v = ref_sigmoid(mix * sc, biasJ, a.hcEps);
             spre[tid] = v;
-            if (a.hPre != nullptr) {
+            if (a.hPre != nullptr && part0) {
                 a.hPre[row * N + tid] = v;
             }
-        } else if (tid < 2 * N) {
-            const float v = ref_sigmoid(mix * sc, biasJ, 0.0f);
-            a.hPost[row * N + (tid - N)] = v * 2.0f;
-        } else {
-            const float v = mix * sc;
-            a.hRes[row * (N * N) + (tid - 2 * N)] = v + biasJ;
+        } else if (part0) {
+            if (tid < 2 * N) {
+                const float v = ref_sigmoid(mix * sc, biasJ, 0.0f);
+                a.hPost[row * N + (tid - N)] = v * 2.0f;
+            } else {
+                const float v = mix * sc;
+                a.hRes[row * (N * N) + (tid - 2 * N)] = v + biasJ;
+            }
         }
     }
     __syncthreads();
@@ -777,7 +786,7 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         pre[s] = spre[s];
     }
     // hIn[d] = RNE(sum over s of pre[s] * x[s][d]), summed in stream order.
-    for (int64_t base = 0; base < DO; base += (int64_t)kEpiThreads * kEpiOct) {
+    for (int64_t base = 0; oBeg + base < oEnd; base += (int64_t)kEpiThreads * kEpiOct) {
         if (base > 0) {
 #pragma unroll
             for (int o = 0; o < kEpiOct; ++o) {
@@ -789,7 +798,7 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         }
 #pragma unroll
         for (int o = 0; o < kEpiOct; ++o) {
-            const int d8 = (int)base + tid + kEpiThreads * o;
+            const int d8 = (int)(oBeg + base) + tid + kEpiThreads * o;
             float acc[8];
             {
                 float f[8];
@@ -814,7 +823,7 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
             for (int w = 0; w < 4; ++w) {
                 out[w] = pack2_x<kBf16>(acc[2 * w], acc[2 * w + 1]);
             }
-            if (d8 < DO) {
+            if (d8 < oEnd) {
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, out), hr,
                     d8 * 16, 0, kCpolNt);
@@ -894,7 +903,14 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
     const bool wide = (p.rowsS + 256 / kCols - 1) / (256 / kCols) > 8;
     for (int64_t r0 = 0; r0 < p.T; r0 += kEpilogueRowsPerLaunch) {
         e.row0 = r0;
-        const dim3 grid((unsigned)std::min<int64_t>(kEpilogueRowsPerLaunch, p.T - r0));
+        const int64_t rows = std::min<int64_t>(kEpilogueRowsPerLaunch, p.T - r0);
+        // Fewer rows than a wave of workgroups (small batches): each row's
+        // hIn is split over up to 8 workgroups of at least 128 column octets
+        // each, so that more CUs share the x reads (each part sums the row's
+        // partials itself; narrow rows gain nothing from a split).
+        const int parts = (int)std::max<int64_t>(
+            1, std::min<int64_t>(std::min<int64_t>(8, 256 / rows), p.D / 8 / 128));
+        const dim3 grid((unsigned)rows, (unsigned)parts);
         if (wide) {
             hipLaunchKernelGGL((rows_epilogue_kernel<N, kBf16, 1024, 1>), grid, dim3(1024), 0, stream, e);
         } else {

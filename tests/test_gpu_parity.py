@@ -330,6 +330,9 @@ def test_shared_workspace_back_to_back(pkg, orc, device, force, expect, n, T, D)
     (20000, 8, 64, True, True),     # 79 row blocks, K = 512: one stage per K-range
     (64, 8, 16384, True, True),     # small-batch GEMM, K = 131072: 512 K-ranges
     (600, 8, 16384, False, True),   # K = 131072 on the block GEMM, fp16
+    (40, 8, 2064, True, False),     # epilogue rows split in 2 parts of 129 / 129 octets
+    (80, 6, 4160, False, True),     # n = 6, 3 parts of 174 / 174 / 172 octets
+    (24, 8, 3088, True, True),      # 3 parts of 129 / 129 / 128 octets
 ])
 def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     """Row-block path (n = 6, 8): ragged row blocks, several K-ranges, fp16 and
