@@ -473,10 +473,19 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     constexpr int Q = C::Q;
     constexpr int COLS = M + 1;
     constexpr int RB = kSmallRows / 16;
-    __shared__ float red[kSmallWaves][kSmallRows][COLS];
+    // LDS: each wave's phi block, staged in row order (row pitch kPhiPitch
+    // floats: consecutive rows start 4 banks apart), then, after a barrier,
+    // the waves' sums.
+    constexpr int kPhiK = kSmallKs * 32;   // phi columns (k) per wave
+    constexpr int kPhiPitch = kPhiK + 4;
+    constexpr int kRedFloats = kSmallWaves * kSmallRows * COLS;
+    constexpr int kStageFloats = kSmallWaves * M * kPhiPitch;
+    __shared__ __attribute__((aligned(16))) float lds[kRedFloats > kStageFloats ? kRedFloats : kStageFloats];
+    float(*red)[kSmallRows][COLS] = reinterpret_cast<float(*)[kSmallRows][COLS]>(lds);
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float *stage = lds + w * (M * kPhiPitch);
     const int kr = blockIdx.x;
     const int T = (int)a.T;
     if (kr == 0 && threadIdx.x == 0) {
@@ -485,39 +494,65 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     const int K2 = (int)(a.K * 2);
     const int64_t ks0 = ((int64_t)kr * kSmallWaves + w) * kSmallKs;  // first k-step of this wave
 
-    // A fragments straight in MFMA layout: lane l holds row 16r + (l & 15)
-    // and the 8 k at 8(l >> 4) of its k-step.
+    // x as whole 128-byte lines (the wave's two k-steps of a row): register
+    // (r, h) holds, in lane l, row 16r + 8h + (l & 7) and the 8 k at
+    // 8(l >> 4) + 32((l >> 3) & 1); a DPP exchange turns each pair into the
+    // A fragments of the two k-steps.
+    static_assert(kSmallKs == 2, "one 128-byte line of each row per wave");
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, T * K2);
-    u32x4_t xa[kSmallKs][RB];
+    u32x4_t xln[RB][2];
 #pragma unroll
-    for (int kk = 0; kk < kSmallKs; ++kk) {
+    for (int r = 0; r < RB; ++r) {
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
-            xa[kk][r] = load16<kCpolNt>(xr, (16 * r + (lane & 15)) * K2 +
-                                                (int)((ks0 + kk) * 64) + 16 * (lane >> 4));
+        for (int h = 0; h < 2; ++h) {
+            xln[r][h] = load16<kCpolNt>(xr, (16 * r + 8 * h + (lane & 7)) * K2 + (int)(ks0 * 64) +
+                                                16 * (lane >> 4) + 64 * ((lane >> 3) & 1));
         }
     }
-    // phi (and gamma) for the B fragments: accumulator tile ta covers mix
-    // columns 16ta + (l & 15); the half tile's lanes 8-15 hold the lo half
-    // of the column of lanes 0-7.
-    f32x4_t ph[kSmallKs][NA][2];
+    // phi rows as whole 256-byte runs (the wave's 64 k of 4 rows per load),
+    // into LDS in row order; read back below in B-fragment order.
+    constexpr int kPhiLoads = M / 4;
+    static_assert(M % 4 == 0, "4 phi rows per load");
+    f32x4_t phl[kPhiLoads];
+#pragma unroll
+    for (int i = 0; i < kPhiLoads; ++i) {
+        const int j = 4 * i + (lane >> 4);
+        phl[i] = *reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + ks0 * 32 + 4 * (lane & 15));
+    }
     f32x4_t gm[kSmallKs][2];
 #pragma unroll
     for (int kk = 0; kk < kSmallKs; ++kk) {
         const int64_t k0 = (ks0 + kk) * 32 + 8 * (lane >> 4);
-#pragma unroll
-        for (int ta = 0; ta < NA; ++ta) {
-            const int j = ta < Q ? 16 * ta + (lane & 15) : 16 * Q + (lane & 7);
-            const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + k0);
-            ph[kk][ta][0] = src[0];
-            ph[kk][ta][1] = src[1];
-        }
         const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(a.gamma != nullptr ? a.gamma + k0 : a.phi);
         gm[kk][0] = gsrc[0];
         gm[kk][1] = gsrc[1];
     }
     // Every load is issued before any use: one memory round trip.
     __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int i = 0; i < kPhiLoads; ++i) {
+        *reinterpret_cast<f32x4_t *>(stage + (4 * i + (lane >> 4)) * kPhiPitch + 4 * (lane & 15)) = phl[i];
+    }
+    u32x4_t xa[kSmallKs][RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        lines_to_frags(xln[r][0], xln[r][1], xa[0][r], xa[1][r]);
+    }
+    // B-fragment order: accumulator tile ta covers mix columns 16ta + (l & 15);
+    // the half tile's lanes 8-15 hold the lo half of the column of lanes 0-7.
+    // (The wave reads only its own staging block, which it wrote above.)
+    f32x4_t ph[kSmallKs][NA][2];
+#pragma unroll
+    for (int kk = 0; kk < kSmallKs; ++kk) {
+#pragma unroll
+        for (int ta = 0; ta < NA; ++ta) {
+            const int j = ta < Q ? 16 * ta + (lane & 15) : 16 * Q + (lane & 7);
+            const float *src = stage + j * kPhiPitch + 32 * kk + 8 * (lane >> 4);
+            ph[kk][ta][0] = *reinterpret_cast<const f32x4_t *>(src);
+            ph[kk][ta][1] = *reinterpret_cast<const f32x4_t *>(src + 4);
+        }
+    }
 
     f32x4_t acc[RB][NA];
     f32x4_t gram[RB];
@@ -595,6 +630,8 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
         }
     }
 
+    // Every wave has read its phi block: the LDS now takes the sums.
+    __syncthreads();
     // This wave's sums into LDS (C fragment: lane l, register e holds row
     // 4(l >> 4) + e, column l & 15 of its tile).
 #pragma unroll
