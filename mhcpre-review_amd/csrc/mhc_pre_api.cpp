@@ -369,6 +369,13 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     if (const char *launch = std::getenv("MHCPRE_LAUNCH")) {
         p.fusedCooperative = std::strcmp(launch, "cooperative") == 0;
     }
+    if (const char *spin = std::getenv("MHCPRE_SPIN_LIMIT")) {
+        char *end = nullptr;
+        const unsigned long v = std::strtoul(spin, &end, 10);
+        if (end != spin && *end == '\0' && v <= 0xFFFFFFFFul) {
+            p.spinLimit = static_cast<uint32_t>(v);
+        }
+    }
 
     // Workspace: header, then the split regions and the fused regions, which
     // overlap (one launch at a time per workspace).  Sizes depend on the

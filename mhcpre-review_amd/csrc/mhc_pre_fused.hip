@@ -756,7 +756,7 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
     a.hcEps = p.hcEps;
     a.invFlatDim = p.invFlatDim;
     a.epoch = epoch;
-    a.spinLimit = 1u << 20;  // about a second of polling per wait
+    a.spinLimit = p.spinLimit;
 
     const unsigned lds = (unsigned)fused_lds_bytes<N, KP, kBf16>();
     if (!p.fusedCooperative) {

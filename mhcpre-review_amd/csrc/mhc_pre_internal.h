@@ -46,6 +46,10 @@ struct Plan {
     // guarantees co-residency next to concurrent work at the cost of a
     // slower dispatch (about 20 us per launch on MI355X).
     bool fusedCooperative = false;
+    // Polls of a strip or fused wait before it records kDeviceTimeout and
+    // gives up (about a second).  MHCPRE_SPIN_LIMIT at phase 1 overrides it,
+    // for tests of the timeout path.
+    uint32_t spinLimit = 1u << 20;
     float normEps = 1e-6f;
     float hcEps = 1e-6f;
     float invFlatDim = 0.f;  // fl(1.0f / K), as code/op_host/mhc_pre.cpp:154

@@ -933,7 +933,7 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
     a.hcEps = p.hcEps;
     a.invFlatDim = p.invFlatDim;
     a.epoch = epoch;
-    a.spinLimit = 1u << 20;  // about a second of polling per wait
+    a.spinLimit = p.spinLimit;
     if (!p.fusedCooperative) {
         hipLaunchKernelGGL((strip_kernel<N, kBf16>), dim3((unsigned)p.stripGrid), dim3(kWaves * 64), 0,
                            stream, a);

@@ -375,3 +375,48 @@ def test_epilogue_launches_in_row_chunks(pkg, orc, device, n, want):
     ref = orc.mhc_pre(x[sel], True, phi, alpha, bias, gamma)
     sub = {k: v[sel] for k, v in out.items() if k != "path"}
     check(sub, ref, x[sel], True, orc)
+
+
+@pytest.mark.parametrize("force,n,T,D", [("strip", 4, 2048, 7168), ("fused", 4, 2048, 1024)])
+def test_expired_wait_is_reported_and_cleared(pkg, orc, device, force, n, T, D):
+    """MHCPRE_SPIN_LIMIT=0 at phase 1: a bounded wait between workgroups gives
+    up at its first poll that finds the data missing (the reducer's first
+    poll always does: no record exists yet).  The launch still ends, with
+    invalid outputs, and mhcPreQueryDeviceStatus reports the timeout; a
+    normal executor on the same workspace then runs clean and correct."""
+    import os
+
+    import torch
+
+    K, M = n * D, n * n + 2 * n
+    rng = np.random.default_rng(77)
+    x = to_bits(rng.standard_normal((T, n, D)).astype(np.float32), True)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.full(3, 0.01, dtype=np.float32)
+    bias = rng.uniform(-0.1, 0.1, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    xt, pt, at, bt, gt = to_device(pkg, device, x, True, phi, alpha, bias, gamma)
+    os.environ["MHCPRE_FORCE_PATH"] = force
+    os.environ["MHCPRE_SPIN_LIMIT"] = "0"
+    try:
+        bad = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True)
+    finally:
+        os.environ.pop("MHCPRE_SPIN_LIMIT", None)
+    try:
+        good = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True, workspace=bad.workspace)
+    finally:
+        os.environ.pop("MHCPRE_FORCE_PATH", None)
+    assert bad.path == force and good.path == force
+    _say(f"[timeout] {force} T={T} D={D}")
+    bad.launch()
+    torch.cuda.synchronize()
+    timeout_code = pkg.binding.STATUS_CODE["MHC_STATUS_DEVICE_TIMEOUT"]
+    assert bad.device_status() == timeout_code
+    good.launch()
+    torch.cuda.synchronize()
+    assert good.device_status() == 0
+    # The status word still holds the first launch's timeout, under its epoch.
+    assert bad.device_status() == timeout_code
+    check(fetch(good), orc.mhc_pre(x, True, phi, alpha, bias, gamma), x, True, orc)
+    good.close()
+    bad.close()
