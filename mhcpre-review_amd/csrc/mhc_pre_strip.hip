@@ -562,21 +562,23 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     //    are loaded behind them.
     u32x4_t (*bfr)[NT][64] = bsh[strip];
     constexpr int KW = KS / kGroups;  // k-steps built per wave
+    // Mix columns per lane: hi tile t and lo tile Q + t hold the same column
+    // 16t + (l & 15), so each column is loaded once (NA tiles of columns,
+    // the half tile's lanes 8-15 repeating lanes 0-7).
+    constexpr int NA = Q + (CL::kHalfTile ? 1 : 0);
     const bool hasGamma = a.gamma != nullptr;
-    f32x4_t ph[KW][NT][2];
+    f32x4_t ph[KW][NA][2];
     f32x4_t gm[KW][2];
 #pragma unroll
     for (int i = 0; i < KW; ++i) {
         const int ks = half + kGroups * i;
         const int64_t k0 = (int64_t)(ks >> 1) * a.D + col0 + 32 * (ks & 1) + 8 * grp;
 #pragma unroll
-        for (int ct = 0; ct < NT; ++ct) {
-            bool lo;
-            int jc;
-            CL::slot(16 * ct + rl, lo, jc);
+        for (int ta = 0; ta < NA; ++ta) {
+            const int jc = ta < Q ? 16 * ta + rl : 16 * Q + (rl & 7);
             const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)jc * a.K + k0);
-            ph[i][ct][0] = src[0];
-            ph[i][ct][1] = src[1];
+            ph[i][ta][0] = src[0];
+            ph[i][ta][1] = src[1];
         }
         const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(hasGamma ? a.gamma + k0 : a.phi);
         gm[i][0] = gsrc[0];
@@ -604,21 +606,29 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     for (int i = 0; i < KW; ++i) {
         const int ks = half + kGroups * i;
 #pragma unroll
-        for (int ct = 0; ct < NT; ++ct) {
-            bool lo;
-            int jc;
-            CL::slot(16 * ct + rl, lo, jc);
-            float out[8];
+        for (int ta = 0; ta < NA; ++ta) {
+            float bv[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                float bv = ph[i][ct][e >> 2][e & 3];
+                bv[e] = ph[i][ta][e >> 2][e & 3];
                 if (hasGamma) {
-                    bv = bv * gm[i][e >> 2][e & 3];
+                    bv[e] = bv[e] * gm[i][e >> 2][e & 3];
                 }
-                const float hi = bf16_bits_to_f32(f32_to_bf16_bits(bv));
-                out[e] = lo ? (bv - hi) : hi;
             }
-            bfr[ks][ct][lane] = pack8_bf16(out);
+            u32x4_t hv, lv;  // bf16(B) and bf16(B - hi)
+#pragma unroll
+            for (int w2 = 0; w2 < 4; ++w2) {
+                uint32_t h, l;
+                split2_bf16(bv[2 * w2], bv[2 * w2 + 1], h, l);
+                hv[w2] = h;
+                lv[w2] = l;
+            }
+            if (ta < Q) {
+                bfr[ks][ta][lane] = hv;
+                bfr[ks][Q + ta][lane] = lv;
+            } else {
+                bfr[ks][2 * Q][lane] = rl < 8 ? hv : lv;  // half tile: hi in lanes 0-7
+            }
         }
     }
     lds_barrier();
