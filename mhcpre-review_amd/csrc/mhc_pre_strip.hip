@@ -56,6 +56,8 @@
 #include <stdint.h>
 
 #include <mutex>
+#include <type_traits>
+#include <utility>
 
 namespace mhc {
 namespace {
@@ -202,6 +204,18 @@ __device__ __forceinline__ void record_timeout(const StripArgs &a, int lane)
     if (lane == 0) {
         st_status(a.status, a.epoch);
     }
+}
+
+// Calls f(std::integral_constant<int, i>{}) for i = 0 .. kCount-1.
+template <typename F, int... kIs>
+__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, kIs...>)
+{
+    (f(std::integral_constant<int, kIs>{}), ...);
+}
+template <int kCount, typename F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    static_for_seq(f, std::make_integer_sequence<int, kCount>{});
 }
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also makes every
@@ -652,252 +666,265 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     auto slot_of = [&](int jj) { return teamI * kRingSlots + (kGroups * jj + half) % kRingSlots; };
     bool timedOut = false;
 
-    // Meeting count of the other group once it has run all its steps (each
-    // group runs whole rounds of L steps).
+    // Meeting count of the other group once it has run all its steps.
     const int nmineOther = (nt32 - (half ^ 1) + kGroups - 1) / kGroups;
-    const uint32_t otherCount = 4u * (uint32_t)(((nmineOther + E + L - 1) / L) * L);
+    const uint32_t otherCount = 4u * (uint32_t)(nmineOther + E);
 
-    for (int j0 = 0; j0 < nmine + E; j0 += L) {
-#pragma unroll
-        for (int b = 0; b < L; ++b) {
-            // The step index is recomputed from an opaque copy, so that the
-            // per-step addresses are derived in each step rather than
-            // precomputed for all L unrolled steps and held in registers.
-            int jj = j0 + b;
-            asm volatile("" : "+s"(jj));
-            const int rt = tile_of(jj);
-            const int jh = jj - E;
-            const int hb = (b - E + 2 * L) % L;  // ring slot of own tile jh (static after unrolling)
-            const bool liveH = jh >= 0 && jh < nmine;
-            const int rth = tile_of(jh);
+    // One step of the pipeline: own step j0 + b, ring slot b (a compile-time
+    // constant in every copy of the body).
+    auto step = [&](int j0, auto bc) __attribute__((always_inline)) {
+        constexpr int b = decltype(bc)::value;
+        // The step index is recomputed from an opaque copy, so that the
+        // per-step addresses are derived in each step rather than
+        // precomputed for all L unrolled steps and held in registers.
+        int jj = j0 + b;
+        asm volatile("" : "+s"(jj));
+        const int rt = tile_of(jj);
+        const int jh = jj - E;
+        const int hb = (b - E + 2 * L) % L;  // ring slot of own tile jh (static after unrolling)
+        const bool liveH = jh >= 0 && jh < nmine;
+        const int rth = tile_of(jh);
 
-            // 1. hIn of own tile jh = jj - E from ring slot hb, with hPre
-            //    from the poll issued in the previous step (first the
-            //    fast path: the poll already carries every tag).
-            uint64_t wv = pr[hb];
-            const uint32_t want = bcast_tag((uint32_t)(rth * RC::BWORDS) + (uint32_t)lane, epoch);
-            if (liveH && !timedOut && !__all((uint32_t)(wv >> 32) == want)) {
-                const int blkOff = (slot_of(jh) * RC::BWORDS + lane) * 8;
-                for (uint32_t spins = 0;; ++spins) {
-                    __builtin_amdgcn_s_sleep(1);
-                    wv = ld_word(bcastAll, blkOff);
-                    if (__all((uint32_t)(wv >> 32) == want)) {
-                        break;
+        // 1. hIn of own tile jh = jj - E from ring slot hb, with hPre
+        //    from the poll issued in the previous step (first the
+        //    fast path: the poll already carries every tag).
+        uint64_t wv = pr[hb];
+        const uint32_t want = bcast_tag((uint32_t)(rth * RC::BWORDS) + (uint32_t)lane, epoch);
+        if (liveH && !timedOut && !__all((uint32_t)(wv >> 32) == want)) {
+            const int blkOff = (slot_of(jh) * RC::BWORDS + lane) * 8;
+            for (uint32_t spins = 0;; ++spins) {
+                __builtin_amdgcn_s_sleep(1);
+                wv = ld_word(bcastAll, blkOff);
+                if (__all((uint32_t)(wv >> 32) == want)) {
+                    break;
+                }
+                if (spins >= spinLimit) {
+                    if (lane == 0) {
+                        st_status(statusW, epoch);
                     }
-                    if (spins >= spinLimit) {
-                        if (lane == 0) {
-                            st_status(statusW, epoch);
-                        }
-                        timedOut = true;
-                        break;
-                    }
+                    timedOut = true;
+                    break;
                 }
             }
-            // Lane l holds hPre column l/16 of row l%16.
-            const float preC = __uint_as_float((uint32_t)wv);
-            float pre[2][N];
+        }
+        // Lane l holds hPre column l/16 of row l%16.
+        const float preC = __uint_as_float((uint32_t)wv);
+        float pre[2][N];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int s = 0; s < N; ++s) {
-                    pre[h][s] = __shfl(preC, 16 * s + 8 * h + lrow);
+            for (int s = 0; s < N; ++s) {
+                pre[h][s] = __shfl(preC, 16 * s + 8 * h + lrow);
+            }
+        }
+        u32x4_t hout[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float hv[8];
+#pragma unroll
+            for (int s = 0; s < N; ++s) {
+                float f[8];
+                unpack8<kBf16>(xb[hb][s][h], f);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float prod = pre[h][s] * f[e];
+                    hv[e] = (s == 0) ? prod : hv[e] + prod;
                 }
             }
-            u32x4_t hout[2];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                hout[h][q] = pack2_x<kBf16>(hv[2 * q], hv[2 * q + 1]);
+            }
+        }
+        //    Poll for the hIn of the next step (own tile jh + 1; the
+        //    team's first tile when that does not exist), issued before
+        //    the hIn stores so that the next step's wait for it does not
+        //    also wait for them.
+        {
+            const int jp = jh + 1;
+            const int jpc = (jp >= 0 && jp < nmine) ? jp : 0;
+            pr[(hb + 1) % L] = __builtin_bit_cast(
+                uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
+                              bcastAll, (slot_of(jpc) * RC::BWORDS + lane) * 8, 0, kCpolDev));
+        }
+        {
+            const __amdgpu_buffer_rsrc_t hr = make_rsrc(h_tile(jh), liveH ? rows_of(jh) * Di * 2 : 0);
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                float hv[8];
+                store16<kCpolNt>(hout[h], hr, hLane + 8 * h * Di * 2);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // 2. GEMM of own tile jj (zeros past the last tile) and its Gram
+        //    matrix, one stream at a time; after each stream's MFMAs the
+        //    two loads of that stream of own tile jh + L go out into the
+        //    slot hIn just consumed.
+        const int jn = jh + L;
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(x_tile(jn), rows_of(jn) * Ki * 2);
+        f32x4_t acc[NT];
 #pragma unroll
-                for (int s = 0; s < N; ++s) {
+        for (int t = 0; t < NT; ++t) {
+            acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        // B fragments come from LDS, those of the next k-step read while
+        // this k-step's MFMAs run.
+        u32x4_t bcur[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            bcur[t] = bfr[0][t][lane];
+        }
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+            u32x4_t kf[2];
+            lines_to_frags(xb[b][s][0], xb[b][s][1], kf[0], kf[1]);
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int ks = 2 * s + q;
+                u32x4_t bnext[NT];
+                if (ks + 1 < KS) {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        bnext[t] = bfr[ks + 1][t][lane];
+                    }
+                }
+                if constexpr (kBf16) {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        acc[t] = mfma16(kf[q], bcur[t], acc[t]);
+                    }
+                    gram = mfma16(kf[q], kf[q], gram);
+                } else {
+                    gram = mfma16_f16(kf[q], kf[q], gram);
                     float f[8];
-                    unpack8<kBf16>(xb[hb][s][h], f);
+                    unpack8<kBf16>(kf[q], f);
+                    u32x4_t ahi, alo;
+                    split_f16_to_bf16(f, ahi, alo);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float prod = pre[h][s] * f[e];
-                        hv[e] = (s == 0) ? prod : hv[e] + prod;
+                    for (int t = 0; t < NT; ++t) {
+                        acc[t] = mfma16(ahi, bcur[t], acc[t]);
+                        if (CL::has_hi(t)) {
+                            acc[t] = mfma16(alo, bcur[t], acc[t]);
+                        }
                     }
                 }
+                if (ks + 1 < KS) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    hout[h][q] = pack2_x<kBf16>(hv[2 * q], hv[2 * q + 1]);
-                }
-            }
-            //    Poll for the hIn of the next step (own tile jh + 1; the
-            //    team's first tile when that does not exist), issued before
-            //    the hIn stores so that the next step's wait for it does not
-            //    also wait for them.
-            {
-                const int jp = jh + 1;
-                const int jpc = (jp >= 0 && jp < nmine) ? jp : 0;
-                pr[(hb + 1) % L] = __builtin_bit_cast(
-                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(
-                                  bcastAll, (slot_of(jpc) * RC::BWORDS + lane) * 8, 0, kCpolDev));
-            }
-            {
-                const __amdgpu_buffer_rsrc_t hr = make_rsrc(h_tile(jh), liveH ? rows_of(jh) * Di * 2 : 0);
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    store16<kCpolNt>(hout[h], hr, hLane + 8 * h * Di * 2);
+                    for (int t = 0; t < NT; ++t) {
+                        bcur[t] = bnext[t];
+                    }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-
-            // 2. GEMM of own tile jj (zeros past the last tile) and its Gram
-            //    matrix, one stream at a time; after each stream's MFMAs the
-            //    two loads of that stream of own tile jh + L go out into the
-            //    slot hIn just consumed.
-            const int jn = jh + L;
-            const __amdgpu_buffer_rsrc_t xr = make_rsrc(x_tile(jn), rows_of(jn) * Ki * 2);
-            f32x4_t acc[NT];
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            }
-            f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            // B fragments come from LDS, those of the next k-step read while
-            // this k-step's MFMAs run.
-            u32x4_t bcur[NT];
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                bcur[t] = bfr[0][t][lane];
-            }
-#pragma unroll
-            for (int s = 0; s < N; ++s) {
-                u32x4_t kf[2];
-                lines_to_frags(xb[b][s][0], xb[b][s][1], kf[0], kf[1]);
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const int ks = 2 * s + q;
-                    u32x4_t bnext[NT];
-                    if (ks + 1 < KS) {
-#pragma unroll
-                        for (int t = 0; t < NT; ++t) {
-                            bnext[t] = bfr[ks + 1][t][lane];
-                        }
-                    }
-                    if constexpr (kBf16) {
-#pragma unroll
-                        for (int t = 0; t < NT; ++t) {
-                            acc[t] = mfma16(kf[q], bcur[t], acc[t]);
-                        }
-                        gram = mfma16(kf[q], kf[q], gram);
-                    } else {
-                        gram = mfma16_f16(kf[q], kf[q], gram);
-                        float f[8];
-                        unpack8<kBf16>(kf[q], f);
-                        u32x4_t ahi, alo;
-                        split_f16_to_bf16(f, ahi, alo);
-#pragma unroll
-                        for (int t = 0; t < NT; ++t) {
-                            acc[t] = mfma16(ahi, bcur[t], acc[t]);
-                            if (CL::has_hi(t)) {
-                                acc[t] = mfma16(alo, bcur[t], acc[t]);
-                            }
-                        }
-                    }
-                    if (ks + 1 < KS) {
-#pragma unroll
-                        for (int t = 0; t < NT; ++t) {
-                            bcur[t] = bnext[t];
-                        }
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    xb[hb][s][h] = __builtin_bit_cast(
-                        u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                     xr, xLane + (8 * h * Ki + s * Di) * 2, 0, kCpolNt));
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // Gram diagonal: row r sits in lane 16(r/4) + r, register r % 4.
-            const int di = rl & 3;
-            const float ss = di == 0 ? gram[0] : di == 1 ? gram[1] : di == 2 ? gram[2] : gram[3];
-
-            // 3. This wave's partials into LDS, [column][row]: the C fragment
-            //    gives lane (rl, grp) rows 4grp .. 4grp+3 of column slot 16t + rl.
-            float *mine = &part[half][jj & 1][strip][0];
-#pragma unroll
-            for (int t = 0; t < Q; ++t) {
-                const f32x4_t v = acc[t] + acc[Q + t];
-                *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * t + rl) * kColPitch + 4 * grp) = v;
-            }
-            if constexpr (CL::kHalfTile) {
-                f32x4_t o;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    o[i] = __shfl_xor(acc[2 * Q][i], 8);
-                }
-                if (rl < 8) {
-                    *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * Q + rl) * kColPitch + 4 * grp) =
-                        acc[2 * Q] + o;
-                }
-            }
-            if ((rl >> 2) == grp) {
-                mine[N * kColPitch + rl] = ss;
-            }
-            //    The four strips of this group meet through an LDS counter
-            //    (the other group keeps running): each adds one after its
-            //    partials, then waits for 4 (jj + 1).  A strip writes this
-            //    buffer again two steps later, after the next meeting, by
-            //    which time every strip has read it.  The wait also holds a
-            //    group that is a step ahead of the other (count below 4 jj):
-            //    the SIMDs favour the older waves, and a group left to run
-            //    ahead finishes early and leaves the other to run the last
-            //    steps alone.  The wait for the other group is capped at
-            //    its final count, so it always ends.
-            {
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-                if (lane == 0) {  // one count per wave
-                    __hip_atomic_fetch_add(&arrived[half], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
-                const uint32_t target = 4u * (uint32_t)(jj + 1);
-                const uint32_t otherTarget = min(target - 4u, otherCount);
-                while (__hip_atomic_load(&arrived[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target ||
-                       __hip_atomic_load(&arrived[half ^ 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
-                           otherTarget) {
-                    __builtin_amdgcn_s_sleep(1);
-                }
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-            }
-            // 4. The slice's record: 16-byte chunk c2 = 64 strip + lane
-            //    (column c2/8, rows 2(c2%8), +1), the four strips summed in
-            //    strip order; 8 lanes fill one column's 128-byte line.  Lanes
-            //    past the record and steps past the last tile store out of
-            //    range (dropped).
-            {
-                const int c2 = strip * 64 + lane;
-                const int ch = c2 < RC::CHUNKS ? c2 : 0;
-                const int c = ch >> 3;
-                const int r0 = 2 * (ch & 7);
-                const float *pb = &part[half][jj & 1][0][0];
-                float2 v = *reinterpret_cast<const float2 *>(pb + c * kColPitch + r0);
-#pragma unroll
-                for (int st = 1; st < kStrips; ++st) {
-                    const float2 u =
-                        *reinterpret_cast<const float2 *>(pb + st * RC::COLS * kColPitch + c * kColPitch + r0);
-                    v.x = v.x + u.x;
-                    v.y = v.y + u.y;
-                }
-                const uint32_t pos = (uint32_t)((rt * P32 + p) * RC::WORDS) + (uint32_t)(c * 16 + r0);
-                u32x4_t recw;
-                recw[0] = __float_as_uint(v.x);
-                recw[1] = rec_tag(pos, epoch);
-                recw[2] = __float_as_uint(v.y);
-                recw[3] = rec_tag(pos + 1u, epoch);
-                const __amdgpu_buffer_rsrc_t rr = make_rsrc(
-                    recsBase + ((uint64_t)(uint32_t)slot_of(jj) * (uint32_t)P32 + (uint32_t)p) * RC::WORDS,
-                    jj < nmine ? RC::WORDS * 8 : 0);
-                const int off = c2 < RC::CHUNKS ? 16 * c2 : RC::WORDS * 8;
-                if (local) {
-                    store16<0>(recw, rr, off);
-                } else {
-                    store16<kCpolDev>(recw, rr, off);
-                }
+            for (int h = 0; h < 2; ++h) {
+                xb[hb][s][h] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                 xr, xLane + (8 * h * Ki + s * Di) * 2, 0, kCpolNt));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
+        // Gram diagonal: row r sits in lane 16(r/4) + r, register r % 4.
+        const int di = rl & 3;
+        const float ss = di == 0 ? gram[0] : di == 1 ? gram[1] : di == 2 ? gram[2] : gram[3];
+
+        // 3. This wave's partials into LDS, [column][row]: the C fragment
+        //    gives lane (rl, grp) rows 4grp .. 4grp+3 of column slot 16t + rl.
+        float *mine = &part[half][jj & 1][strip][0];
+#pragma unroll
+        for (int t = 0; t < Q; ++t) {
+            const f32x4_t v = acc[t] + acc[Q + t];
+            *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * t + rl) * kColPitch + 4 * grp) = v;
+        }
+        if constexpr (CL::kHalfTile) {
+            f32x4_t o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                o[i] = __shfl_xor(acc[2 * Q][i], 8);
+            }
+            if (rl < 8) {
+                *reinterpret_cast<f32x4_t *>(mine + RC::col(16 * Q + rl) * kColPitch + 4 * grp) =
+                    acc[2 * Q] + o;
+            }
+        }
+        if ((rl >> 2) == grp) {
+            mine[N * kColPitch + rl] = ss;
+        }
+        //    The four strips of this group meet through an LDS counter
+        //    (the other group keeps running): each adds one after its
+        //    partials, then waits for 4 (jj + 1).  A strip writes this
+        //    buffer again two steps later, after the next meeting, by
+        //    which time every strip has read it.  The wait also holds a
+        //    group that is a step ahead of the other (count below 4 jj):
+        //    the SIMDs favour the older waves, and a group left to run
+        //    ahead finishes early and leaves the other to run the last
+        //    steps alone.  The wait for the other group is capped at
+        //    its final count, so it always ends.
+        {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            if (lane == 0) {  // one count per wave
+                __hip_atomic_fetch_add(&arrived[half], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            const uint32_t target = 4u * (uint32_t)(jj + 1);
+            const uint32_t otherTarget = min(target - 4u, otherCount);
+            while (__hip_atomic_load(&arrived[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target ||
+                   __hip_atomic_load(&arrived[half ^ 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                       otherTarget) {
+                __builtin_amdgcn_s_sleep(1);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        }
+        // 4. The slice's record: 16-byte chunk c2 = 64 strip + lane
+        //    (column c2/8, rows 2(c2%8), +1), the four strips summed in
+        //    strip order; 8 lanes fill one column's 128-byte line.  Lanes
+        //    past the record and steps past the last tile store out of
+        //    range (dropped).
+        {
+            const int c2 = strip * 64 + lane;
+            const int ch = c2 < RC::CHUNKS ? c2 : 0;
+            const int c = ch >> 3;
+            const int r0 = 2 * (ch & 7);
+            const float *pb = &part[half][jj & 1][0][0];
+            float2 v = *reinterpret_cast<const float2 *>(pb + c * kColPitch + r0);
+#pragma unroll
+            for (int st = 1; st < kStrips; ++st) {
+                const float2 u =
+                    *reinterpret_cast<const float2 *>(pb + st * RC::COLS * kColPitch + c * kColPitch + r0);
+                v.x = v.x + u.x;
+                v.y = v.y + u.y;
+            }
+            const uint32_t pos = (uint32_t)((rt * P32 + p) * RC::WORDS) + (uint32_t)(c * 16 + r0);
+            u32x4_t recw;
+            recw[0] = __float_as_uint(v.x);
+            recw[1] = rec_tag(pos, epoch);
+            recw[2] = __float_as_uint(v.y);
+            recw[3] = rec_tag(pos + 1u, epoch);
+            const __amdgpu_buffer_rsrc_t rr = make_rsrc(
+                recsBase + ((uint64_t)(uint32_t)slot_of(jj) * (uint32_t)P32 + (uint32_t)p) * RC::WORDS,
+                jj < nmine ? RC::WORDS * 8 : 0);
+            const int off = c2 < RC::CHUNKS ? 16 * c2 : RC::WORDS * 8;
+            if (local) {
+                store16<0>(recw, rr, off);
+            } else {
+                store16<kCpolDev>(recw, rr, off);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Whole rounds of L steps; then the last, partial round, whose steps past
+    // the drain are skipped (a separate copy of the body, so that the branch
+    // does not reach the main loop).
+    int j0 = 0;
+    for (; j0 + L <= nmine + E; j0 += L) {
+        static_for<L>([&](auto bc) __attribute__((always_inline)) { step(j0, bc); });
+    }
+    if (j0 < nmine + E) {
+        static_for<L>([&](auto bc) __attribute__((always_inline)) {
+            if (j0 + decltype(bc)::value < nmine + E) {
+                step(j0, bc);
+            }
+        });
     }
 }
 
