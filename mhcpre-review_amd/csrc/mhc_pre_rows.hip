@@ -52,6 +52,8 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 namespace mhc {
 namespace {
@@ -113,6 +115,18 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Calls f(std::integral_constant<int, i>{}) for i = 0 .. kCount-1.
+template <typename F, int... kIs>
+__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, kIs...>)
+{
+    (f(std::integral_constant<int, kIs>{}), ...);
+}
+template <int kCount, typename F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    static_for_seq(f, std::make_integer_sequence<int, kCount>{});
 }
 
 // A fragments of k-steps 2q and 2q + 1 from line-layout registers r0 (rows
@@ -336,77 +350,91 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
     // wave's stash of B(s) visible and tells every wave that all reads of
     // LDS slot (s + 1) mod 2 (stage s - 1) are done; B(s + 1) goes there,
     // and stage s + kAhead's loads go out into the staging set and ring slot
-    // just freed.  The trip count is rounded up to whole trips: the stages
-    // past the K-range read zeros for both x and B, and add nothing.
-    const int nstTrips = (nst + kUnroll - 1) / kUnroll * kUnroll;
-    for (int s0 = 0; s0 < nstTrips; s0 += kUnroll) {
+    // just freed.  Loads of stages past the K-range read zeros for both x
+    // and B.
+    // One step, stage s0 + u, with u (the ring and staging slots) a
+    // compile-time constant in every copy of the body.
+    auto step = [&](int s0, auto uc) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value;
+        const int s = s0 + u;
+        const int sl = u % kXSlots;
+        const int bl = u % 2;
+        wait_vm<kXLoads + (kAhead - 2) * (NB + kXLoads)>();
+        lds_barrier();
+        stash((u + 1) % 2, bst[(u + 1) % kBSets]);
+        issue(s + kAhead, bst[(u + kAhead) % kBSets], xs[(u + kAhead) % kXSlots]);
+        if (vrows > 0) {
+            // All of the stage's B fragments are read before its MFMAs,
+            // so the LDS latency is paid once per stage.
+            u32x4_t bf[kStageKs][NT];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int s = s0 + u;
-            const int sl = u % kXSlots;
-            const int bl = u % 2;
-            wait_vm<kXLoads + (kAhead - 2) * (NB + kXLoads)>();
-            lds_barrier();
-            stash((u + 1) % 2, bst[(u + 1) % kBSets]);
-            issue(s + kAhead, bst[(u + kAhead) % kBSets], xs[(u + kAhead) % kXSlots]);
-            if (vrows > 0) {
-                // All of the stage's B fragments are read before its MFMAs,
-                // so the LDS latency is paid once per stage.
-                u32x4_t bf[kStageKs][NT];
+            for (int ksl = 0; ksl < kStageKs; ++ksl) {
 #pragma unroll
-                for (int ksl = 0; ksl < kStageKs; ++ksl) {
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        bf[ksl][t] = bsh[bl][ksl * NT + t][lane];
-                    }
+                for (int t = 0; t < NT; ++t) {
+                    bf[ksl][t] = bsh[bl][ksl * NT + t][lane];
                 }
-                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int c = 0; c < kLines; ++c) {
-                    u32x4_t af[2][2];  // [16-row block][k-step of the line]
-                    lines_to_frags(xs[sl][0][c], xs[sl][1][c], af[0][0], af[0][1]);
-                    lines_to_frags(xs[sl][2][c], xs[sl][3][c], af[1][0], af[1][1]);
+            for (int c = 0; c < kLines; ++c) {
+                u32x4_t af[2][2];  // [16-row block][k-step of the line]
+                lines_to_frags(xs[sl][0][c], xs[sl][1][c], af[0][0], af[0][1]);
+                lines_to_frags(xs[sl][2][c], xs[sl][3][c], af[1][0], af[1][1]);
 #pragma unroll
-                    for (int kk = 0; kk < 2; ++kk) {
-                        const int ksl = 2 * c + kk;
-                        if constexpr (kBf16) {
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int ksl = 2 * c + kk;
+                    if constexpr (kBf16) {
 #pragma unroll
-                            for (int t = 0; t < NT; ++t) {
-                                const u32x4_t b = bf[ksl][t];
-                                acc[0][C::acc(t)] = mfma16(af[0][kk], b, acc[0][C::acc(t)]);
-                                acc[1][C::acc(t)] = mfma16(af[1][kk], b, acc[1][C::acc(t)]);
-                            }
-                            gram[0] = mfma16(af[0][kk], af[0][kk], gram[0]);
-                            gram[1] = mfma16(af[1][kk], af[1][kk], gram[1]);
-                        } else {
-                            // fp16 x = hi + lo exactly in bf16; x_lo meets the
-                            // hi B columns only (x_lo * B_lo is below 2^-16 of
-                            // the product).
-                            u32x4_t xh[2], xl[2];
+                        for (int t = 0; t < NT; ++t) {
+                            const u32x4_t b = bf[ksl][t];
+                            acc[0][C::acc(t)] = mfma16(af[0][kk], b, acc[0][C::acc(t)]);
+                            acc[1][C::acc(t)] = mfma16(af[1][kk], b, acc[1][C::acc(t)]);
+                        }
+                        gram[0] = mfma16(af[0][kk], af[0][kk], gram[0]);
+                        gram[1] = mfma16(af[1][kk], af[1][kk], gram[1]);
+                    } else {
+                        // fp16 x = hi + lo exactly in bf16; x_lo meets the
+                        // hi B columns only (x_lo * B_lo is below 2^-16 of
+                        // the product).
+                        u32x4_t xh[2], xl[2];
+#pragma unroll
+                        for (int r = 0; r < 2; ++r) {
+                            float fx[8];
+                            unpack8<false>(af[r][kk], fx);
+                            split_f16_to_bf16(fx, xh[r], xl[r]);
+                        }
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) {
+                            const u32x4_t b = bf[ksl][t];
 #pragma unroll
                             for (int r = 0; r < 2; ++r) {
-                                float fx[8];
-                                unpack8<false>(af[r][kk], fx);
-                                split_f16_to_bf16(fx, xh[r], xl[r]);
-                            }
-#pragma unroll
-                            for (int t = 0; t < NT; ++t) {
-                                const u32x4_t b = bf[ksl][t];
-#pragma unroll
-                                for (int r = 0; r < 2; ++r) {
-                                    acc[r][C::acc(t)] = mfma16(xh[r], b, acc[r][C::acc(t)]);
-                                    if (C::hi_tile(t)) {
-                                        acc[r][C::acc(t)] = mfma16(xl[r], b, acc[r][C::acc(t)]);
-                                    }
+                                acc[r][C::acc(t)] = mfma16(xh[r], b, acc[r][C::acc(t)]);
+                                if (C::hi_tile(t)) {
+                                    acc[r][C::acc(t)] = mfma16(xl[r], b, acc[r][C::acc(t)]);
                                 }
                             }
-                            gram[0] = mfma16_f16(af[0][kk], af[0][kk], gram[0]);
-                            gram[1] = mfma16_f16(af[1][kk], af[1][kk], gram[1]);
                         }
+                        gram[0] = mfma16_f16(af[0][kk], af[0][kk], gram[0]);
+                        gram[1] = mfma16_f16(af[1][kk], af[1][kk], gram[1]);
                     }
                 }
             }
         }
+    };
+    // Whole trips of kUnroll stages; then the last, partial trip as a second
+    // copy of the body that skips the stages past the K-range (the same for
+    // every wave of the workgroup), so that the branch stays out of the main
+    // loop.
+    int s0 = 0;
+    for (; s0 + kUnroll <= nst; s0 += kUnroll) {
+        static_for<kUnroll>([&](auto uc) __attribute__((always_inline)) { step(s0, uc); });
+    }
+    if (s0 < nst) {
+        static_for<kUnroll>([&](auto uc) __attribute__((always_inline)) {
+            if (s0 + decltype(uc)::value < nst) {
+                step(s0, uc);
+            }
+        });
     }
     // Loads of the stages past the K-range may still be in flight.
     __builtin_amdgcn_s_waitcnt(0);
