@@ -330,7 +330,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         // Small batches: one K-range per workgroup of the small-batch GEMM,
         // which builds B from phi itself (each element of B is used once).
         const int64_t smallKs = mhc::rows_small_ksteps();
-        if (T <= mhc::rows_small_rows() && ((K / 32) % smallKs) == 0 &&
+        if (T <= mhc::rows_small_rows(n) && ((K / 32) % smallKs) == 0 &&
             T * K * 2 < (int64_t{1} << 31)) {
             p.rowsSmall = true;
             p.rowsS = static_cast<int>((K / 32) / smallKs);

@@ -82,7 +82,7 @@ struct Plan {
     // rows_block_rows() rows.
     int rowsS = 0;
     int rowsBlocks = 0;
-    // Small batches (T <= rows_small_rows()): one GEMM workgroup per K-range
+    // Small batches (T <= rows_small_rows(n)): one GEMM workgroup per K-range
     // of rows_small_ksteps() k-steps, B built from phi in registers, no prep.
     bool rowsSmall = false;
 
@@ -125,7 +125,7 @@ int rows_block_rows();
 int rows_stage_ksteps();
 int rows_gemm_threads();
 // Largest batch of the small-batch GEMM and k-steps per workgroup there.
-int rows_small_rows();
+int rows_small_rows(int n);
 int rows_small_ksteps();
 
 // Workgroups of the strip kernel that can be resident per CU (x numCUs), or

@@ -67,7 +67,10 @@ constexpr int kStageKs = 2;                  // k-steps per stage (kStageKs / 2 
 constexpr int kAhead = 3;                    // stages of x loading ahead of the MFMAs
 constexpr int kXSlots = kAhead + 1;          // x register ring
 constexpr int kBSets = kAhead - 1;           // B staging register sets
-constexpr int kSmallRows = 64;               // small-batch GEMM: rows held by every wave
+// Small-batch GEMM: rows held by every wave (n = 4 has 2 accumulator tiles
+// per 16 rows, n = 6 and 8 have 3 and 5).
+template <int N>
+constexpr int small_rows() { return N == 4 ? 128 : 64; }
 constexpr int kSmallWaves = 4;               // small-batch GEMM: waves splitting a K-range
 constexpr int kSmallKs = 2;                  // small-batch GEMM: k-steps per wave
 
@@ -500,6 +503,7 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     constexpr int NA = C::NA;
     constexpr int Q = C::Q;
     constexpr int COLS = M + 1;
+    constexpr int kSmallRows = small_rows<N>();
     constexpr int RB = kSmallRows / 16;
     // LDS: each wave's phi block, staged in row order (row pitch kPhiPitch
     // floats: consecutive rows start 4 banks apart), then, after a barrier,
@@ -993,7 +997,7 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
 
 int rows_block_rows() { return kRowBlock; }
 int rows_gemm_threads() { return kRW * 64; }
-int rows_small_rows() { return kSmallRows; }
+int rows_small_rows(int n) { return n == 4 ? small_rows<4>() : n == 6 ? small_rows<6>() : small_rows<8>(); }
 int rows_small_ksteps() { return kSmallWaves * kSmallKs; }
 int rows_stage_ksteps() { return kStageKs; }
 

@@ -333,6 +333,8 @@ def test_shared_workspace_back_to_back(pkg, orc, device, force, expect, n, T, D)
     (40, 8, 2064, True, False),     # epilogue rows split in 2 parts of 129 / 129 octets
     (80, 6, 4160, False, True),     # n = 6, 3 parts of 174 / 174 / 172 octets
     (24, 8, 3088, True, True),      # 3 parts of 129 / 129 / 128 octets
+    (100, 4, 256, False, False),    # n = 4 small-batch GEMM (128 rows per wave), 100 rows
+    (128, 4, 7168, True, True),     # n = 4 small-batch GEMM, full 128 rows, K = 28672
 ])
 def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     """Row-block path (n = 6, 8): ragged row blocks, several K-ranges, fp16 and
