@@ -30,6 +30,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 COPY_BYTES = 256 << 20  # size of the calibration copy (--copy-probe)
+CEILING_BYTES = 512 << 20  # size of the copy whose rate is reported as the measured ceiling
 
 WORKLOADS = {
     # name: (n, D, T, bf16, gamma, outlier rows x50)
@@ -195,6 +196,25 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
+    # Measured ceiling: a plain device-to-device copy of 512 MiB (read + write
+    # bytes over its event-timed duration, median of 5, after 2 untimed
+    # copies), beside the spec peak.  It runs after the timed region.
+    csrc = torch.empty(CEILING_BYTES // 4, dtype=torch.float32, device=device).fill_(1.0)
+    cdst = torch.empty_like(csrc)
+    for _ in range(2):
+        cdst.copy_(csrc)
+    cts = []
+    for _ in range(5):
+        c0 = torch.cuda.Event(enable_timing=True)
+        c1 = torch.cuda.Event(enable_timing=True)
+        c0.record(stream)
+        cdst.copy_(csrc)
+        c1.record(stream)
+        torch.cuda.synchronize()
+        cts.append(c0.elapsed_time(c1))
+    copy_gbs = 2 * CEILING_BYTES / (sorted(cts)[len(cts) // 2] * 1e-3) / 1e9
+    del csrc, cdst
+
     b_alg = algorithmic_bytes(n, D, T, bf16, gamma_on)
     achieved = b_alg / (mean_ms * 1e-3) / 1e9
     workload = (f"mhc_pre n={n} D={D} T={T} {'bf16' if bf16 else 'fp16'} "
@@ -222,7 +242,8 @@ def main() -> int:
                    "traffic_source": traffic["summary"] if traffic else None},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic["traffic_bytes"] if traffic else None},
+                     "traffic": traffic["traffic_bytes"] if traffic else None,
+                     "copy_ceiling": copy_gbs, "frac_of_copy": achieved / copy_gbs},
     }
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_baseline(x, phi, alpha, bias, gamma, bf16,
