@@ -19,7 +19,7 @@
  * addresses; phase 2 launches on a HIP stream.  The caller owns every device
  * buffer, including the workspace, whose contents need not be preserved
  * between launches.  An executor's plan is immutable after creation (it only
- * records the epoch of its latest launch, for mhcPreQueryDeviceStatus): it may
+ * records the id of its latest launch, for mhcPreQueryDeviceStatus): it may
  * be launched any number of times (the reference probe relaunches one
  * executor, cloud_runner/probe_e1e2.cpp:312-326) and from several host threads
  * on different streams, provided the launches do not share a workspace
@@ -127,11 +127,17 @@ MHC_API int mhcPreGetWorkspaceSizeWithHPre(const mhcTensor *x, const mhcTensor *
  * The strip and fused kernels' workgroups wait on each other (bounded), so
  * their grids are sized to what the device holds at once.  By default it is a
  * plain launch: every workgroup is resident unless another kernel occupies the
- * device at the same time, in which case a wait can expire and
- * mhcPreQueryDeviceStatus reports MHC_STATUS_DEVICE_TIMEOUT (no hang).  With
+ * device at the same time, in which case a wait can expire: the launch still
+ * ends (no hang), mhcPre has already returned MHC_STATUS_SUCCESS, the rows
+ * whose wait expired hold NaN in hIn / hPre / hPost / hRes (never a plausible
+ * value), and mhcPreQueryDeviceStatus reports MHC_STATUS_DEVICE_TIMEOUT.  With
  * the environment variable MHCPRE_LAUNCH=cooperative at phase 1 the executor
  * uses a cooperative launch, which guarantees co-residency next to concurrent
  * work but dispatches more slowly (about 20 us per launch on MI355X).
+ *
+ * A launch may be captured into a HIP graph and replayed: the exchange epoch
+ * that tells the current launch's data from stale workspace contents is kept
+ * in the workspace itself and advanced by every launch, replays included.
  */
 MHC_API int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor,
            hipStream_t stream);

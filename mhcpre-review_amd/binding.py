@@ -197,6 +197,10 @@ class MhcPreOp:
         else:
             self.workspace = torch.empty(max(self.workspace_size, 256), dtype=torch.uint8,
                                          device=dev)
+        # Launch arguments that stay fixed for the executor's lifetime.
+        self._dev_index = self.workspace.device.index
+        self._ws_ptr = ctypes.c_void_p(self.workspace.data_ptr())
+        self._ws_size = ctypes.c_uint64(self.workspace_size)
 
     @property
     def path(self) -> str:
@@ -206,17 +210,34 @@ class MhcPreOp:
             raise MhcPreError("mhcPreExecutorPath", st)
         return name.value.decode()
 
-    def launch(self, stream=None) -> None:
+    def launch(self, stream=None, check: bool = False) -> None:
+        """Enqueue one launch (phase 2) on ``stream`` (default: the current
+        stream of the tensors' device).  With ``check=True`` the call then
+        synchronizes the stream and raises MhcPreError(MHC_STATUS_DEVICE_TIMEOUT)
+        if a bounded wait between workgroups expired; the rows that wait was
+        for hold NaN in every output in that case, never a plausible value."""
         import torch
 
         # The library launches on the current device, which must hold the
         # tensors; the default stream is that device's current stream.
-        with torch.cuda.device(self.workspace.device):
-            st = self.lib.mhcPre(ctypes.c_void_p(self.workspace.data_ptr()),
-                                 ctypes.c_uint64(self.workspace_size), self.executor,
+        if torch.cuda.current_device() != self._dev_index:
+            with torch.cuda.device(self._dev_index):
+                st = self.lib.mhcPre(self._ws_ptr, self._ws_size, self.executor,
+                                     ctypes.c_void_p(_stream_handle(stream)))
+        else:
+            st = self.lib.mhcPre(self._ws_ptr, self._ws_size, self.executor,
                                  ctypes.c_void_p(_stream_handle(stream)))
         if st != 0:
             raise MhcPreError("mhcPre", st)
+        if check:
+            self.check(stream)
+
+    def check(self, stream=None) -> None:
+        """Synchronize ``stream`` and raise if this executor's latest launch
+        reported an expired wait (mhcPreQueryDeviceStatus)."""
+        st = self.device_status(stream)
+        if st != 0:
+            raise MhcPreError("mhcPreQueryDeviceStatus", st)
 
     def device_status(self, stream=None) -> int:
         return self.lib.mhcPreQueryDeviceStatus(ctypes.c_void_p(self.workspace.data_ptr()),
@@ -241,13 +262,14 @@ class MhcPreOp:
 
 def mhc_pre(x, phi, alpha, bias, gamma=None, norm_eps: float = 1e-6, hc_eps: float = 1e-6,
             h_pre: bool = False, stream=None):
-    """One call: returns (hIn, hPost, hRes, hPre-or-None) after the launch is enqueued."""
+    """One call: returns (hIn, hPost, hRes, hPre-or-None) once the launch has
+    finished.  The workspace must outlive the launch, so this call waits for
+    the stream anyway, and checks the device status on the way: an expired
+    wait between workgroups raises MhcPreError."""
     op = MhcPreOp(x, phi, alpha, bias, gamma, norm_eps, hc_eps, h_pre=True if h_pre else None)
-    op.launch(stream)
-    # The workspace must outlive the launch: hold it until the stream is idle.
-    import torch
-
-    torch.cuda.current_stream().synchronize() if stream is None else stream.synchronize()
-    outs = op.outputs()
-    op.close()
+    try:
+        op.launch(stream, check=True)
+    finally:
+        outs = op.outputs()
+        op.close()
     return outs

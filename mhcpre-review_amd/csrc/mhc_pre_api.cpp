@@ -28,9 +28,14 @@ struct mhcPreExecutor {
     // Device that holds x (-1: the runtime could not tell, e.g. no device is
     // visible at phase 1); launches must have it current.
     int device = -1;
-    // Epoch of this executor's latest launch; the device status word only
+    // Host id of this executor's latest launch; the device status word only
     // reports a timeout written under it.
-    std::atomic<uint32_t> lastEpoch{0};
+    std::atomic<uint32_t> lastLaunchId{0};
+    // Workgroups of the strip / fused kernel the device holds at once
+    // (occupancy query, made once per executor: at phase 1 when the current
+    // device holds x, else at the first launch); -2 until known.
+    std::atomic<int> stripCoresident{-2};
+    std::atomic<int> fusedCoresident{-2};
 };
 
 namespace {
@@ -120,10 +125,10 @@ int device_of(const void *p)
     return attr.type == hipMemoryTypeDevice ? attr.device : -1;
 }
 
-// Launch epochs: process-wide, strictly increasing from a start that differs
-// between processes (time and address mixed), skipping 0 and ~0 so that a
-// zero- or one-filled workspace can never carry a valid tag.
-uint32_t next_epoch()
+// Launch ids (written into the status word with a timeout): process-wide,
+// strictly increasing from a start that differs between processes (time and
+// address mixed), skipping 0 and ~0.
+uint32_t next_launch_id()
 {
     static std::atomic<uint32_t> counter{[] {
         const uint64_t t = static_cast<uint64_t>(
@@ -420,6 +425,8 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     return MHC_STATUS_SUCCESS;
 }
 
+void prime_coresident(mhcPreExecutor *ex);
+
 int get_workspace(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alpha,
                   const mhcTensor *bias, const mhcTensor *gamma, float normEps, float hcEps,
                   const mhcTensor *hIn, const mhcTensor *hPost, const mhcTensor *hRes,
@@ -441,9 +448,122 @@ int get_workspace(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alp
     }
     ex->plan = plan;
     ex->device = device_of(plan.x);
+    prime_coresident(ex);
     *workspaceSize = plan.wsTotal;
     *executor = ex;
     return MHC_STATUS_SUCCESS;
+}
+
+// Co-resident workgroups of the executor's strip or fused kernel on the
+// current device: the occupancy query runs once per executor and kernel.
+int cached_coresident(std::atomic<int> &slot, int (*query)(const mhc::Plan &, int),
+                      const mhc::Plan &p, int cus)
+{
+    int v = slot.load(std::memory_order_relaxed);
+    if (v == -2) {
+        v = query(p, cus);
+        slot.store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+// Phase 2 after the workspace checks: the device check, the path choice for
+// this device and the kernel launches.
+int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
+{
+    const mhc::Plan &p = executor->plan;
+    // The kernels run on the current device and address the executor's
+    // tensors directly: it must be the device that holds them.
+    if (executor->device >= 0) {
+        int current = -1;
+        if (hipGetDevice(&current) != hipSuccess) {
+            (void)hipGetLastError();
+            return MHC_STATUS_HIP_ERROR;
+        }
+        if (current != executor->device) {
+            return MHC_STATUS_DEVICE_MISMATCH;
+        }
+    }
+    hipError_t err = hipSuccess;
+    bool done = false;
+    int device = -1;
+    DeviceShape shape;
+    // The launches' status is read back with hipGetLastError: first clear an
+    // error an earlier call of the process may have left there (the split
+    // path makes no other HIP call before its first launch).
+    (void)hipGetLastError();
+    if (p.path != mhc::Path::kSplit && !device_shape(device, shape)) {
+        return MHC_STATUS_HIP_ERROR;
+    }
+    const uint32_t launchId = next_launch_id();
+    executor->lastLaunchId.store(launchId, std::memory_order_relaxed);
+    if (p.path == mhc::Path::kStrip) {
+        // One workgroup per CU, all co-resident; each XCD's CUs hold at least
+        // one team of stripP slice workgroups and one reducer workgroup.
+        const int perXcd = shape.cus / shape.xcds;
+        int teamsPerXcd = perXcd / (p.stripP + 1);
+        // Teams beyond the rings' capacity would have no slots of their own
+        // (teams without tiles write nothing).
+        if (teamsPerXcd * shape.xcds > p.stripMaxTeams && p.stripMaxTeams < p.fusedTiles) {
+            teamsPerXcd = p.stripMaxTeams / shape.xcds;
+        }
+        if (teamsPerXcd >= 1 &&
+            cached_coresident(executor->stripCoresident, mhc::strip_max_coresident, p, shape.cus) >=
+                shape.cus) {
+            mhc::Plan lp = p;
+            lp.stripXcds = shape.xcds;
+            lp.stripTeamsPerXcd = teamsPerXcd;
+            // Workgroups of a team beyond the slices and reducers leave at once.
+            lp.stripR = mhc::strip_reducers(perXcd / teamsPerXcd - p.stripP);
+            lp.stripGrid = shape.cus;
+            err = mhc::launch_strip(lp, workspace, launchId, stream);
+            done = true;
+        }
+    }
+    if (!done && p.fusedP > 0 && (p.path == mhc::Path::kFused || p.path == mhc::Path::kStrip)) {
+        // The fused path, or the strip path's fallback on a device too small
+        // for a strip team.  Teams of fusedP workgroups must be co-resident; a
+        // device too small for one team runs the split path instead.
+        const int coresident =
+            cached_coresident(executor->fusedCoresident, mhc::fused_max_coresident, p, shape.cus);
+        if (coresident >= p.fusedP) {
+            mhc::Plan lp = p;
+            lp.fusedTeams = coresident / p.fusedP;
+            lp.fusedGrid = lp.fusedTeams * p.fusedP;
+            err = mhc::launch_fused(lp, workspace, launchId, stream);
+            done = true;
+        }
+    }
+    if (!done && p.path == mhc::Path::kRows) {
+        err = mhc::launch_rows(p, workspace, shape.xcds, stream);
+        done = true;
+    }
+    if (!done) {
+        err = mhc::launch_split(p, workspace, stream);
+    }
+    return err == hipSuccess ? MHC_STATUS_SUCCESS : MHC_STATUS_HIP_ERROR;
+}
+
+// The occupancy queries of a new executor, when the current device is the
+// one that holds its tensors (otherwise its first launch makes them).
+void prime_coresident(mhcPreExecutor *ex)
+{
+    const mhc::Plan &p = ex->plan;
+    int device = -1;
+    DeviceShape shape;
+    if (ex->device < 0 || (p.path != mhc::Path::kStrip && p.path != mhc::Path::kFused)) {
+        return;
+    }
+    if (!device_shape(device, shape) || device != ex->device) {
+        (void)hipGetLastError();
+        return;
+    }
+    if (p.path == mhc::Path::kStrip) {
+        (void)cached_coresident(ex->stripCoresident, mhc::strip_max_coresident, p, shape.cus);
+    }
+    if (p.fusedP > 0) {
+        (void)cached_coresident(ex->fusedCoresident, mhc::fused_max_coresident, p, shape.cus);
+    }
 }
 
 }  // namespace
@@ -476,84 +596,13 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
     if (executor == nullptr) {
         return MHC_STATUS_NULL_ARGUMENT;
     }
-    const mhc::Plan &p = executor->plan;
-    if (workspace == nullptr || workspaceSize < p.wsTotal) {
+    if (workspace == nullptr || workspaceSize < executor->plan.wsTotal) {
         return MHC_STATUS_WORKSPACE_TOO_SMALL;
     }
     if (!aligned(workspace, 256)) {
         return MHC_STATUS_WORKSPACE_TOO_SMALL;
     }
-    // The kernels run on the current device and address the executor's
-    // tensors directly: it must be the device that holds them.
-    if (executor->device >= 0) {
-        int current = -1;
-        if (hipGetDevice(&current) != hipSuccess) {
-            (void)hipGetLastError();
-            return MHC_STATUS_HIP_ERROR;
-        }
-        if (current != executor->device) {
-            return MHC_STATUS_DEVICE_MISMATCH;
-        }
-    }
-    hipError_t err = hipSuccess;
-    bool done = false;
-    int device = -1;
-    DeviceShape shape;
-    // The launches' status is read back with hipGetLastError: first clear an
-    // error an earlier call of the process may have left there (the split
-    // path makes no other HIP call before its first launch).
-    (void)hipGetLastError();
-    if (p.path != mhc::Path::kSplit && !device_shape(device, shape)) {
-        return MHC_STATUS_HIP_ERROR;
-    }
-    if (p.path == mhc::Path::kStrip) {
-        // One workgroup per CU, all co-resident; each XCD's CUs hold at least
-        // one team of stripP slice workgroups and one reducer workgroup.
-        const int perXcd = shape.cus / shape.xcds;
-        int teamsPerXcd = perXcd / (p.stripP + 1);
-        // Teams beyond the rings' capacity would have no slots of their own
-        // (teams without tiles write nothing).
-        if (teamsPerXcd * shape.xcds > p.stripMaxTeams && p.stripMaxTeams < p.fusedTiles) {
-            teamsPerXcd = p.stripMaxTeams / shape.xcds;
-        }
-        if (teamsPerXcd >= 1 && mhc::strip_max_coresident(p, shape.cus) >= shape.cus) {
-            mhc::Plan lp = p;
-            lp.stripXcds = shape.xcds;
-            lp.stripTeamsPerXcd = teamsPerXcd;
-            // Workgroups of a team beyond the slices and reducers leave at once.
-            lp.stripR = mhc::strip_reducers(perXcd / teamsPerXcd - p.stripP);
-            lp.stripGrid = shape.cus;
-            const uint32_t epoch = next_epoch();
-            executor->lastEpoch.store(epoch, std::memory_order_relaxed);
-            err = mhc::launch_strip(lp, workspace, epoch, stream);
-            done = true;
-        }
-    }
-    if (!done && p.fusedP > 0 && (p.path == mhc::Path::kFused || p.path == mhc::Path::kStrip)) {
-        // The fused path, or the strip path's fallback on a device too small
-        // for a strip team.  Teams of fusedP workgroups must be co-resident; a
-        // device too small for one team runs the split path instead.
-        const int coresident = mhc::fused_max_coresident(p, shape.cus);
-        if (coresident >= p.fusedP) {
-            mhc::Plan lp = p;
-            lp.fusedTeams = coresident / p.fusedP;
-            lp.fusedGrid = lp.fusedTeams * p.fusedP;
-            const uint32_t epoch = next_epoch();
-            executor->lastEpoch.store(epoch, std::memory_order_relaxed);
-            err = mhc::launch_fused(lp, workspace, epoch, stream);
-            done = true;
-        }
-    }
-    if (!done && p.path == mhc::Path::kRows) {
-        executor->lastEpoch.store(next_epoch(), std::memory_order_relaxed);
-        err = mhc::launch_rows(p, workspace, shape.xcds, stream);
-        done = true;
-    }
-    if (!done) {
-        executor->lastEpoch.store(next_epoch(), std::memory_order_relaxed);
-        err = mhc::launch_split(p, workspace, stream);
-    }
-    return err == hipSuccess ? MHC_STATUS_SUCCESS : MHC_STATUS_HIP_ERROR;
+    return launch_on(workspace, executor, stream);
 }
 
 int mhcPreExecutorDestroy(mhcPreExecutor *executor)
@@ -584,7 +633,7 @@ int mhcPreQueryDeviceStatus(void *workspace, uint64_t workspaceSize,
     const uint32_t code = static_cast<uint32_t>(word);
     const uint32_t epoch = static_cast<uint32_t>(word >> 32);
     const bool timedOut = code == mhc::kDeviceTimeout &&
-                          epoch == executor->lastEpoch.load(std::memory_order_relaxed);
+                          epoch == executor->lastLaunchId.load(std::memory_order_relaxed);
     return timedOut ? MHC_STATUS_DEVICE_TIMEOUT : MHC_STATUS_SUCCESS;
 }
 

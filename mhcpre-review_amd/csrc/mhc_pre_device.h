@@ -167,6 +167,49 @@ __device__ __forceinline__ void split_f16_to_bf16(const float (&f)[8], u32x4_t &
     }
 }
 
+// Exchange epoch of a strip or fused launch, kept in the workspace header.
+// One thread of every workgroup reads the epoch the previous launch on the
+// workspace stored (epoch_load) and the launch uses epoch_next of it, so
+// consecutive launches on a workspace, graph replays included, never share an
+// epoch.  After its last read of the header every workgroup reports once
+// (epoch_finish); the report that completes the grid stores the new epoch.
+// The completion word pairs the epoch with a count, so a workspace left with
+// any contents by other use needs no reset.
+__device__ __forceinline__ uint32_t epoch_next(uint32_t prev)
+{
+    const uint32_t e = prev + 1u;
+    return (e == 0u || e == 0xFFFFFFFFu) ? 1u : e;  // 0 and ~0 never tag a word
+}
+
+__device__ __forceinline__ uint32_t epoch_load(void *ws, size_t epochOff)
+{
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(static_cast<char *>(ws) + epochOff, (short)0, 4, 0x00020000);
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 16 /* sc1 */);
+}
+
+__device__ __forceinline__ void epoch_finish(void *ws, size_t epochOff, size_t doneOff, uint32_t epoch,
+                                             uint32_t grid)
+{
+    uint64_t *done = reinterpret_cast<uint64_t *>(static_cast<char *>(ws) + doneOff);
+    uint32_t *ep = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + epochOff);
+    uint64_t old = __hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+        const uint32_t cnt = (uint32_t)(old >> 32) == epoch ? (uint32_t)old + 1u : 1u;
+        const uint64_t next = ((uint64_t)epoch << 32) | cnt;
+        if (__hip_atomic_compare_exchange_strong(done, &old, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)) {
+            if (cnt == grid) {
+                __hip_atomic_store(ep, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+    }
+}
+
+// Quiet NaN written into the outputs of rows whose exchange wait expired.
+__device__ __forceinline__ float poison() { return __uint_as_float(0x7FC00000u); }
+
 // Sigmoid in the reference vector order (code/op_kernel/mhc_pre.cpp:542-555):
 // scale, +bias, negate, exp, +1, reciprocal, +eps (only when eps != 0).
 __device__ __forceinline__ float ref_sigmoid(float scaled, float bias, float eps)

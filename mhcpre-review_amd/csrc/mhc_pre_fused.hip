@@ -38,9 +38,12 @@
 // value exactly when its tag matches: no arrival counter, no release wait and
 // no reset of the workspace between launches.  A reader accepts a block only
 // when every word it read carries the expected tag; a block left over from an
-// earlier launch (another epoch) or filled with any constant never does.
-// Every wait is bounded by a spin limit; running out records kDeviceTimeout
-// with the launch's epoch in the status word instead of hanging.  The grid is
+// earlier launch (another epoch) or filled with any constant never does.  The
+// epoch is kept in the workspace header (epoch_load / epoch_finish), so the
+// replays of a captured HIP graph get fresh epochs too.  Every wait is bounded
+// by a spin limit; running out records kDeviceTimeout with the host launch id
+// in the status word instead of hanging, and the values that wait was for are
+// taken as NaN, so the affected outputs are NaN.  The grid is
 // sized to the device's co-residency limit, so every workgroup is resident
 // when nothing else runs on the device (a cooperative launch, on request,
 // guarantees it even then); a reducer is then never waiting on a workgroup
@@ -73,7 +76,8 @@ struct FusedArgs {
     float *hPre;
     uint64_t *recs;      // [RT][P] records of Rec<N>::WORDS tagged words
     uint64_t *bcast;     // [RT] blocks of Rec<N>::BWORDS tagged words
-    uint64_t *status;    // (epoch << 32) | kDeviceTimeout after a timeout
+    uint64_t *status;    // (launchId << 32) | kDeviceTimeout after a timeout
+    char *hdr;           // workspace header (status word, exchange epoch)
     int64_t T;
     int64_t D;
     int64_t K;
@@ -83,7 +87,7 @@ struct FusedArgs {
     float normEps;
     float hcEps;
     float invFlatDim;
-    uint32_t epoch;
+    uint32_t launchId;
     uint32_t spinLimit;
 };
 
@@ -230,7 +234,7 @@ __device__ __forceinline__ f32x4_t mfma16_f16(const u32x4_t &a, const u32x4_t &b
 __device__ __forceinline__ void record_timeout(const FusedArgs &a, int lane)
 {
     if (lane == 0) {
-        __hip_atomic_store(a.status, ((uint64_t)a.epoch << 32) | kDeviceTimeout, __ATOMIC_RELAXED,
+        __hip_atomic_store(a.status, ((uint64_t)a.launchId << 32) | kDeviceTimeout, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -248,17 +252,26 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     constexpr int DW = 64 * KP;
     constexpr int Q = CL::Q;
     extern __shared__ u32x4_t bl[];  // [N*KS][NT][64] B fragments, per-wave scratch, staging
+    __shared__ uint32_t epochSh;     // the launch's exchange epoch, from thread 0 to every wave
     static_assert(N == 4, "the fused path maps the n = 4 hPre columns to the 4 lane groups");
 
+    const int tid = threadIdx.x;
+    // Thread 0 reads the epoch the previous launch on this workspace left.
+    const uint32_t prevEpoch = tid == 0 ? epoch_load(a.hdr, kWsEpochOff) : 0u;
+    auto finish = [&](uint32_t epoch) {
+        if (tid == 0) {
+            epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch, gridDim.x);
+        }
+    };
     const int P = a.P;
     const int numTeams = a.numTeams;
     const int g = blockIdx.x;
     if (g >= P * numTeams) {
+        finish(epoch_next(prevEpoch));
         return;  // spare workgroup: the whole workgroup leaves together
     }
     const int team = g % numTeams;
     const int p = g / numTeams;
-    const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int64_t d0 = (int64_t)p * DW;
@@ -281,6 +294,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
             u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xLane + 128 * kp, so, kCpolNt));
     };
     if ((int64_t)team * W >= a.RT) {
+        finish(epoch_next(prevEpoch));
         return;  // no row tile for any wave of this workgroup
     }
     if (rt < a.RT) {
@@ -363,12 +377,15 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
             }
         }
     }
+    if (tid == 0) {
+        epochSh = epoch_next(prevEpoch);
+    }
     __syncthreads();
 
     const float alphaPre = a.alpha[0];
     const float alphaPost = a.alpha[1];
     const float alphaRes = a.alpha[2];
-    const uint32_t epoch = a.epoch;
+    const uint32_t epoch = __builtin_amdgcn_readfirstlane(epochSh);
 
     // hPost / hRes columns (mix columns N .. M-1) of a finished tile: column
     // N + m is done by slice m mod P, from the records (every one of them is
@@ -388,6 +405,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
                 }
                 if (spins >= a.spinLimit) {
                     record_timeout(a, laneO);
+                    tot = make_float2(poison(), poison());  // an expired wait: NaN outputs
                     break;
                 }
                 __builtin_amdgcn_s_sleep(2);
@@ -566,6 +584,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
                 }
                 if (spins >= a.spinLimit) {
                     record_timeout(a, laneO);
+                    tot = make_float2(poison(), poison());  // NaN hPre, invRms and outputs
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
@@ -616,6 +635,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
                 }
                 if (spins >= a.spinLimit) {
                     record_timeout(a, laneO);
+                    pw = iw = (uint64_t)__float_as_uint(poison());  // NaN hIn, hPost, hRes
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
@@ -687,6 +707,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     if (prevTile >= 0) {
         post_res(prevTile, prevInvRms, P, lane);
     }
+    finish(epoch);
 }
 
 template <int N, int KP, bool kBf16>
@@ -726,7 +747,7 @@ int fused_coresident_t(int numCUs)
 }
 
 template <int N, int KP, bool kBf16>
-hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t epoch, hipStream_t stream)
+hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t launchId, hipStream_t stream)
 {
     hipError_t err = fused_prepare_attr<N, KP, kBf16>();
     if (err != hipSuccess) {
@@ -744,6 +765,7 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
     a.hRes = p.hRes;
     a.hPre = p.hasHPre ? p.hPre : nullptr;
     a.status = reinterpret_cast<uint64_t *>(ws);
+    a.hdr = ws;
     a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsFinal);
     a.recs = reinterpret_cast<uint64_t *>(ws + p.wsFusedPartial);
     a.T = p.T;
@@ -755,7 +777,7 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
     a.normEps = p.normEps;
     a.hcEps = p.hcEps;
     a.invFlatDim = p.invFlatDim;
-    a.epoch = epoch;
+    a.launchId = launchId;
     a.spinLimit = p.spinLimit;
 
     const unsigned lds = (unsigned)fused_lds_bytes<N, KP, kBf16>();
@@ -785,12 +807,12 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
         break;                                                                 \
     }
 
-hipError_t launch_fused(const Plan &p, void *workspace, uint32_t epoch, hipStream_t stream)
+hipError_t launch_fused(const Plan &p, void *workspace, uint32_t launchId, hipStream_t stream)
 {
     if (p.n != 4) {
         return hipErrorNotSupported;
     }
-    MHC_FUSED_DISPATCH(launch_fused_t, p, workspace, epoch, stream)
+    MHC_FUSED_DISPATCH(launch_fused_t, p, workspace, launchId, stream)
     return hipErrorNotSupported;
 }
 

@@ -16,14 +16,22 @@ enum class Path : int {
 };
 
 // Device status word (first 8 bytes of the workspace): the low half holds a
-// code, the high half the epoch of the launch that wrote it.  The fused path
-// writes (epoch, kDeviceTimeout) only when a wait runs out; the split path's
-// first kernel writes kDeviceOk into the low half.
+// code, the high half the host launch id of the launch that wrote it.  The
+// strip and fused kernels write (launch id, kDeviceTimeout) only when a wait
+// runs out; the split path's first kernel writes kDeviceOk into the low half.
 constexpr uint32_t kDeviceOk = 0u;
 constexpr uint32_t kDeviceTimeout = 0x7107u;
 
-// Bytes reserved at the head of the workspace for the status word.
+// Bytes reserved at the head of the workspace: the status word at 0, and the
+// exchange epoch of the strip and fused kernels.  The epoch lives in device
+// memory, not in the kernel arguments, so that a launch captured in a HIP
+// graph still gets a fresh epoch on every replay: every workgroup reads the
+// word at kWsEpochOff and uses one more than it; the last workgroup of the
+// grid to finish (counted in the word at kWsDoneOff, which pairs the epoch
+// with the number of finished workgroups) stores the new epoch back.
 constexpr size_t kWsHeaderBytes = 256;
+constexpr size_t kWsEpochOff = 64;   // uint32: epoch of the latest strip / fused launch
+constexpr size_t kWsDoneOff = 128;   // uint64: (epoch << 32) | finished workgroups
 
 struct Plan {
     Path path = Path::kSplit;
@@ -110,11 +118,12 @@ struct Plan {
 
 // Kernel launchers (mhc_pre_kernels.hip).  Each returns the first HIP error.
 hipError_t launch_split(const Plan &plan, void *workspace, hipStream_t stream);
-// epoch: per-launch value mixed into the fused path's exchange tags; it must
-// differ from the epoch of every earlier launch that used this workspace.
-hipError_t launch_fused(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
+// launchId: host-side id of the launch, written with kDeviceTimeout into the
+// status word when a bounded wait expires (the exchange epoch itself comes
+// from the workspace header).
+hipError_t launch_fused(const Plan &plan, void *workspace, uint32_t launchId, hipStream_t stream);
 
-hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t epoch, hipStream_t stream);
+hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t launchId, hipStream_t stream);
 
 // Rows path (mhc_pre_rows.hip); nXcd: XCDs of the device (work placement
 // only).

@@ -44,10 +44,13 @@
 // atomic accesses at device scope (sc1).  The tag is a hash of the word's
 // position XOR a per-launch epoch, so a word holds the current value exactly
 // when its tag matches: no arrival counter, no release wait, no reset of the
-// workspace between launches.  Every wait is bounded by a spin limit; running
-// out records kDeviceTimeout with the launch's epoch in the status word
-// instead of hanging.  The grid is one workgroup per CU, all co-resident when
-// nothing else occupies the device.
+// workspace between launches.  The epoch is kept in the workspace header
+// (epoch_load / epoch_finish), so replays of a captured HIP graph get fresh
+// epochs too.  Every wait is bounded by a spin limit; running out records
+// kDeviceTimeout with the host launch id in the status word instead of
+// hanging, and the rows the wave or workgroup could not finish get NaN
+// outputs.  The grid is one workgroup per CU, all co-resident when nothing
+// else occupies the device.
 
 #include "mhc_pre_device.h"
 #include "mhc_pre_internal.h"
@@ -101,7 +104,8 @@ struct StripArgs {
     float *hPre;
     uint64_t *recs;    // [team][ringSlots][P] records of Rec<N>::WORDS tagged words
     uint64_t *bcast;   // [team][ringSlots] blocks of Rec<N>::BWORDS tagged words
-    uint64_t *status;  // (epoch << 32) | kDeviceTimeout after a timeout
+    uint64_t *status;  // (launchId << 32) | kDeviceTimeout after a timeout
+    char *hdr;         // workspace header (status word, exchange epoch)
     int64_t T;
     int64_t D;
     int64_t K;
@@ -114,7 +118,7 @@ struct StripArgs {
     float normEps;
     float hcEps;
     float invFlatDim;
-    uint32_t epoch;
+    uint32_t launchId;
     uint32_t spinLimit;
 };
 
@@ -185,9 +189,9 @@ __device__ __forceinline__ uint64_t ld_word(__amdgpu_buffer_rsrc_t r, int off)
 {
     return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCpolDev));
 }
-__device__ __forceinline__ void st_status(uint64_t *status, uint32_t epoch)
+__device__ __forceinline__ void st_status(uint64_t *status, uint32_t launchId)
 {
-    const uint64_t v = ((uint64_t)epoch << 32) | kDeviceTimeout;
+    const uint64_t v = ((uint64_t)launchId << 32) | kDeviceTimeout;
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, v),
                                           make_rsrc(status, 8), 0, 0, kCpolDev);
 }
@@ -202,7 +206,7 @@ __device__ __forceinline__ void store16(const u32x4_t &v, __amdgpu_buffer_rsrc_t
 __device__ __forceinline__ void record_timeout(const StripArgs &a, int lane)
 {
     if (lane == 0) {
-        st_status(a.status, a.epoch);
+        st_status(a.status, a.launchId);
     }
 }
 
@@ -309,7 +313,8 @@ struct ColPoll {
 
 template <int N>
 __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int ntiles, int r, int R,
-                                           bool local, float *lds)
+                                           bool local, float *lds, uint32_t prevEpoch,
+                                           uint32_t *epochSh)
 {
     using RC = Rec<N>;
     constexpr int COLS = RC::COLS;
@@ -323,7 +328,13 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
     float *irs = lds + 2 * kSums;     // [16] invRms per row
     const int tid = threadIdx.x;
     const int P = a.P;
-    const uint32_t epoch = a.epoch;
+    // The launch's exchange epoch: read by thread 0 from the workspace header
+    // (prevEpoch), handed to every wave through LDS.
+    if (tid == 0) {
+        *epochSh = epoch_next(prevEpoch);
+    }
+    lds_barrier();
+    const uint32_t epoch = __builtin_amdgcn_readfirstlane(*epochSh);
     const float alphaPre = a.alpha[0];
     const float alphaPost = a.alpha[1];
     const float alphaRes = a.alpha[2];
@@ -337,15 +348,22 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
         const int rt = team + a.numTeams * k;
         const uint32_t slot = (uint32_t)(team * kRingSlots + k % kRingSlots);
         const __amdgpu_buffer_rsrc_t tr = make_rsrc(a.recs + (uint64_t)slot * P * RC::WORDS, P * RC::WORDS * 8);
-        const uint32_t tileBase = (uint32_t)(rt * P * RC::WORDS);
+        const uint32_t tileBase = (uint32_t)rt * (uint32_t)P * (uint32_t)RC::WORDS;
 
-        // Phase 1: hPre columns and sum of squares.
+        // Phase 1: hPre columns and sum of squares.  Once a wait of this
+        // workgroup has expired, its rows get NaN outputs (and a NaN hPre
+        // broadcast, so the slices' hIn of those rows is NaN too).
         float2 acc;
+        bool got = false;  // every word of this tile's columns carried its tag
         for (uint32_t spins = 0;; ++spins) {
             p1.issue(tr, P);
             const bool ok = p1.sum(tileBase, epoch, P, acc);
-            if (__syncthreads_and(ok) != 0 || timedOut) {
+            if (__syncthreads_and(ok) != 0) {
+                got = true;
                 break;
+            }
+            if (timedOut) {
+                break;  // an earlier wait expired: no more waiting in this launch
             }
             if (spins >= a.spinLimit) {
                 record_timeout(a, tid);
@@ -353,6 +371,9 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
+        }
+        if (!got) {
+            acc = make_float2(poison(), poison());
         }
         if (p1.act) {
             sums[(p1.sg * Poll1::ITEMS + tid % Poll1::ITEMS) * 2] = acc.x;
@@ -384,7 +405,7 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
                 const float v = ref_sigmoid(mix * (ir * alphaPre), bias1, a.hcEps);
                 const int idx = c * 16 + p1.r0 + e;
                 wv[2 * e] = __float_as_uint(v);
-                wv[2 * e + 1] = bcast_tag((uint32_t)(rt * RC::BWORDS) + idx, epoch);
+                wv[2 * e + 1] = bcast_tag((uint32_t)rt * (uint32_t)RC::BWORDS + (uint32_t)idx, epoch);
                 const int row = rt * 16 + p1.r0 + e;
                 if (a.hPre != nullptr && row < a.T) {
                     a.hPre[(int64_t)row * N + c] = v;
@@ -399,10 +420,15 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
         }
 
         // Phase 2: hPost / hRes columns.
+        got = false;
         for (uint32_t spins = 0;; ++spins) {
             p2.issue(tr, P);
             const bool ok = p2.sum(tileBase, epoch, P, acc);
-            if (__syncthreads_and(ok) != 0 || timedOut) {
+            if (__syncthreads_and(ok) != 0) {
+                got = true;
+                break;
+            }
+            if (timedOut) {
                 break;
             }
             if (spins >= a.spinLimit) {
@@ -411,6 +437,9 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
+        }
+        if (!got) {
+            acc = make_float2(poison(), poison());
         }
         if (p2.act) {
             sums[(p2.sg * Poll2::ITEMS + tid % Poll2::ITEMS) * 2] = acc.x;
@@ -444,6 +473,9 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
         }
         lds_barrier();  // sums / irs are reused by the next tile
     }
+    if (tid == 0) {
+        epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch, gridDim.x);
+    }
 }
 
 template <int N, bool kBf16>
@@ -469,18 +501,27 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     __shared__ u32x4_t bsh[kStrips][KS][NT][64];
     // Per-group count of partials written (4 per own step).
     __shared__ uint32_t arrived[kGroups];
+    // The launch's exchange epoch, handed from thread 0 to every wave.
+    __shared__ uint32_t epochSh;
 
+    const int tid = threadIdx.x;
+    // Thread 0 reads the epoch the previous launch on this workspace left; the
+    // load is waited for only where the epoch is first needed.
+    const uint32_t prevEpoch = tid == 0 ? epoch_load(a.hdr, kWsEpochOff) : 0u;
     const int g = blockIdx.x;
     const int xcd = g % a.nXcd;
     const int j = g / a.nXcd;
     const int teamSize = a.P + a.R;
     const int tj = j / teamSize;
     if (tj >= a.teamsPerXcd) {
-        return;  // spare workgroup: the whole workgroup leaves together
+        // Spare workgroup: the whole workgroup leaves together.
+        if (tid == 0) {
+            epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch_next(prevEpoch), gridDim.x);
+        }
+        return;
     }
     const int team = xcd + a.nXcd * tj;
     const int role = j % teamSize;
-    const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) wave index
     const int64_t numTeams = a.numTeams;
@@ -493,7 +534,8 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const bool local = a.nXcd > 1 && (int)(__builtin_amdgcn_s_getreg(kXccIdReg) & 15) == xcd;
 
     if (role >= a.P) {
-        reducer_wg<N>(a, team, (int)ntiles, role - a.P, a.R, local, &part[0][0][0][0]);
+        reducer_wg<N>(a, team, (int)ntiles, role - a.P, a.R, local, &part[0][0][0][0], prevEpoch,
+                      &epochSh);
         return;
     }
 
@@ -514,11 +556,13 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const int hLane = (lrow * Di + col0 + lineOff) * 2;
     const int rl = lane & 15;
     const int grp = lane >> 4;
-    const uint32_t epoch = a.epoch;
     if (tid < kGroups) {
         arrived[tid] = 0;
     }
     if (ntiles == 0) {
+        if (tid == 0) {
+            epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch_next(prevEpoch), gridDim.x);
+        }
         return;
     }
     // 32-bit tile and row indices (the launch validates T < 2^31 / 16);
@@ -534,8 +578,9 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     uint64_t *statusW = a.status;
     int P32 = a.P;
     uint32_t spinLimit = a.spinLimit;
+    uint32_t launchId = a.launchId;
     asm volatile("" : "+s"(xBase), "+s"(hBase), "+s"(recsBase), "+s"(bcastBase), "+s"(statusW),
-                 "+s"(P32), "+s"(spinLimit));
+                 "+s"(P32), "+s"(spinLimit), "+s"(launchId));
     const int nt32 = (int)ntiles;
     const int nmine = (nt32 - half + kGroups - 1) / kGroups;
     const int teamI = team;
@@ -645,7 +690,11 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             }
         }
     }
+    if (tid == 0) {
+        epochSh = epoch_next(prevEpoch);
+    }
     lds_barrier();
+    const uint32_t epoch = __builtin_amdgcn_readfirstlane(epochSh);
 
     // Every step issues the same memory operations in the same order (two
     // hIn stores, one broadcast poll, eight x loads, one record store per
@@ -689,7 +738,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         //    from the poll issued in the previous step (first the
         //    fast path: the poll already carries every tag).
         uint64_t wv = pr[hb];
-        const uint32_t want = bcast_tag((uint32_t)(rth * RC::BWORDS) + (uint32_t)lane, epoch);
+        const uint32_t want = bcast_tag((uint32_t)rth * (uint32_t)RC::BWORDS + (uint32_t)lane, epoch);
         if (liveH && !timedOut && !__all((uint32_t)(wv >> 32) == want)) {
             const int blkOff = (slot_of(jh) * RC::BWORDS + lane) * 8;
             for (uint32_t spins = 0;; ++spins) {
@@ -700,15 +749,17 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 }
                 if (spins >= spinLimit) {
                     if (lane == 0) {
-                        st_status(statusW, epoch);
+                        st_status(statusW, launchId);
                     }
                     timedOut = true;
                     break;
                 }
             }
         }
-        // Lane l holds hPre column l/16 of row l%16.
-        const float preC = __uint_as_float((uint32_t)wv);
+        // Lane l holds hPre column l/16 of row l%16.  Once a wait of this
+        // wave has expired its hPre is taken as NaN, so the hIn of those
+        // rows is NaN rather than a value from a missing broadcast.
+        const float preC = timedOut ? poison() : __uint_as_float((uint32_t)wv);
         float pre[2][N];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -894,7 +945,8 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 v.x = v.x + u.x;
                 v.y = v.y + u.y;
             }
-            const uint32_t pos = (uint32_t)((rt * P32 + p) * RC::WORDS) + (uint32_t)(c * 16 + r0);
+            const uint32_t pos = ((uint32_t)rt * (uint32_t)P32 + (uint32_t)p) * (uint32_t)RC::WORDS +
+                                 (uint32_t)(c * 16 + r0);
             u32x4_t recw;
             recw[0] = __float_as_uint(v.x);
             recw[1] = rec_tag(pos, epoch);
@@ -926,6 +978,9 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             }
         });
     }
+    if (tid == 0) {
+        epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch, gridDim.x);
+    }
 }
 
 template <int N, bool kBf16>
@@ -941,7 +996,7 @@ int strip_coresident_t(int numCUs)
 }
 
 template <int N, bool kBf16>
-hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t epoch, hipStream_t stream)
+hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t launchId, hipStream_t stream)
 {
     char *ws = static_cast<char *>(workspace);
     StripArgs a;
@@ -955,6 +1010,7 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
     a.hRes = p.hRes;
     a.hPre = p.hasHPre ? p.hPre : nullptr;
     a.status = reinterpret_cast<uint64_t *>(ws);
+    a.hdr = ws;
     a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsFinal);
     a.recs = reinterpret_cast<uint64_t *>(ws + p.wsFusedPartial);
     a.T = p.T;
@@ -969,7 +1025,7 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
     a.normEps = p.normEps;
     a.hcEps = p.hcEps;
     a.invFlatDim = p.invFlatDim;
-    a.epoch = epoch;
+    a.launchId = launchId;
     a.spinLimit = p.spinLimit;
     if (!p.fusedCooperative) {
         hipLaunchKernelGGL((strip_kernel<N, kBf16>), dim3((unsigned)p.stripGrid), dim3(kWaves * 64), 0,
@@ -986,13 +1042,13 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t epoch, hipStr
 
 }  // namespace
 
-hipError_t launch_strip(const Plan &p, void *workspace, uint32_t epoch, hipStream_t stream)
+hipError_t launch_strip(const Plan &p, void *workspace, uint32_t launchId, hipStream_t stream)
 {
     if (p.n != 4) {
         return hipErrorNotSupported;
     }
-    return p.isBf16 ? launch_strip_t<4, true>(p, workspace, epoch, stream)
-                    : launch_strip_t<4, false>(p, workspace, epoch, stream);
+    return p.isBf16 ? launch_strip_t<4, true>(p, workspace, launchId, stream)
+                    : launch_strip_t<4, false>(p, workspace, launchId, stream);
 }
 
 int strip_ring_slots() { return kRingSlots; }

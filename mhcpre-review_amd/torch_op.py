@@ -19,6 +19,7 @@ operator is forward-only).
 """
 from __future__ import annotations
 
+import os
 from typing import Optional
 
 import torch
@@ -28,12 +29,20 @@ from .binding import MhcPreOp
 _LIB_NAME = "mhcpre"
 
 
+def _check_status() -> bool:
+    # MHCPRE_CHECK_STATUS=1: every launch waits for its stream and raises
+    # MhcPreError(MHC_STATUS_DEVICE_TIMEOUT) if a bounded wait between
+    # workgroups expired.  Off by default (it synchronizes); without it such a
+    # launch leaves NaN in the outputs of the rows it could not finish.
+    return os.environ.get("MHCPRE_CHECK_STATUS", "") not in ("", "0")
+
+
 def _launch(x, phi, alpha, bias, gamma, norm_eps, hc_eps, with_h_pre):
     args = [t.contiguous() for t in (x, phi, alpha, bias)]
     g = gamma.contiguous() if gamma is not None else None
     op = MhcPreOp(*args, g, norm_eps, hc_eps, h_pre=True if with_h_pre else None)
     try:
-        op.launch()
+        op.launch(check=_check_status())
     finally:
         # The executor is host data; the workspace tensor returns to the caching
         # allocator when `op` goes, in the order of the current stream, after

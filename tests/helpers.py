@@ -98,6 +98,9 @@ def assert_hin(got_bits, want_bits, x_bits, is_bf16: bool, got_pre, want_pre, or
         dpre = ATOL + RTOL * wp
     d = ulp_distance(got_bits, want_bits)
     far = d > HIN_MAX_ULP
+    # How many elements use the hPre-propagation allowance, and how far.
+    print(f"[hin-allowance] {int(far.sum())}/{far.size} elements beyond {HIN_MAX_ULP} ulp "
+          f"(max {int(d.max()) if d.size else 0} ulp)", flush=True)
     if far.any():
         xf = np.abs(_decode16(x_bits, is_bf16))                      # [R, n, D]
         n = xf.shape[1]

@@ -1,12 +1,13 @@
 """Full-size configurations (headline prefill and the ragged n=8 case).
 
-Inputs of this size are generated on the GPU (seeded torch generator).  Two
+Inputs of this size are generated on the GPU (seeded torch generator).  Three
 independent checks:
   * sampled rows (first, last -- including the ragged tail tile -- random, and
     every x50 outlier row) against the CPU oracle;
-  * every row against a float64 restatement of the formula evaluated with
-    torch on the GPU (GEMM in fp64, epilogue in fp64); hIn is checked from the
-    kernel's own hPre with an fp64 stream sum.
+  * every row's hPre / hPost / hRes against a float64 restatement of the
+    formula evaluated with torch on the GPU (GEMM and epilogue in fp64);
+  * every row's hIn bit for bit against the reference's stream order evaluated
+    with torch on the GPU from the kernel's own hPre.
 """
 from __future__ import annotations
 
@@ -92,20 +93,24 @@ def test_full_size(pkg, orc, device, cfg):
         tol = 1e-5 + 1e-4 * want.abs()
         bad = int((err > tol).sum())
         assert bad == 0, f"{name}: {bad} values beyond tolerance vs fp64 (max err {err.max():.3e})"
-    # hIn from the kernel's own hPre, summed in fp64: the kernel's fp32 sum of
-    # n rounded products differs from it by far less than one output ulp, so
-    # after rounding the two agree to 1 ulp except at exact-tie boundaries.
-    hin64 = (h_pre.double()[:, :, None] * x64.reshape(T, n, D)).sum(1)
-    hin_ref = hin64.float().to(x.dtype).view(torch.int16)
-
-    def ordered(v):  # sign-magnitude 16-bit patterns -> value order
-        v = v.int() & 0xFFFF
-        mag = v & 0x7FFF
-        return torch.where((v & 0x8000) != 0, -mag, mag)
-
-    dist = (ordered(h_in) - ordered(hin_ref)).abs()
-    far = int((dist > 1).sum())
-    assert far <= h_in.numel() // 100000, f"hIn vs fp64 stream sum: {far} beyond 1 ulp"
+    # hIn on every row, bit for bit, from the kernel's own hPre: products
+    # fl(hPre[s] * x[s]) in fp32, summed over s = 0 .. n-1 in that order in
+    # fp32, rounded half-even to the output dtype -- the reference's stream
+    # order (code/op_kernel/mhc_pre.cpp:787-813, the oracle's
+    # weighted_stream_sum).  Each torch elementwise op is one IEEE rounding.
+    xs = x.reshape(T, n, D)
+    acc = h_pre[:, 0:1].float() * xs[:, 0, :].float()
+    for s_ in range(1, n):
+        acc = acc + h_pre[:, s_:s_ + 1].float() * xs[:, s_, :].float()
+    want_hin = acc.to(x.dtype).view(torch.int16)
+    del acc
+    # The restatement agrees with the oracle's stream sum on the sampled rows.
+    sampled = want_hin[rows_t].cpu().numpy().view(np.uint16)
+    assert np.array_equal(sampled, orc.weighted_stream_sum(
+        x_rows, case.is_bf16, h_pre[rows_t].cpu().numpy()))
+    neq = int((h_in != want_hin).sum())
+    _say(f"[fullsize] hIn rows {T}: {neq} elements differ from the stream sum on the device hPre")
+    assert neq == 0, f"hIn: {neq} of {h_in.numel()} elements differ from the reference stream order"
     del x64, mix
 
     # 3) Relaunch: bitwise identical.

@@ -382,10 +382,12 @@ def test_epilogue_launches_in_row_chunks(pkg, orc, device, n, want):
 @pytest.mark.parametrize("force,n,T,D", [("strip", 4, 2048, 7168), ("fused", 4, 2048, 1024)])
 def test_expired_wait_is_reported_and_cleared(pkg, orc, device, force, n, T, D):
     """MHCPRE_SPIN_LIMIT=0 at phase 1: a bounded wait between workgroups gives
-    up at its first poll that finds the data missing (the reducer's first
-    poll always does: no record exists yet).  The launch still ends, with
-    invalid outputs, and mhcPreQueryDeviceStatus reports the timeout; a
-    normal executor on the same workspace then runs clean and correct."""
+    up at its first poll that finds the data missing (a reducer's first poll
+    finds no record yet).  The launch still ends; every output element it
+    could not finish is NaN and every other one is exactly the clean value;
+    mhcPreQueryDeviceStatus reports the timeout and launch(check=True)
+    raises.  A normal executor on the same workspace then runs clean and
+    correct."""
     import os
 
     import torch
@@ -410,15 +412,89 @@ def test_expired_wait_is_reported_and_cleared(pkg, orc, device, force, n, T, D):
         os.environ.pop("MHCPRE_FORCE_PATH", None)
     assert bad.path == force and good.path == force
     _say(f"[timeout] {force} T={T} D={D}")
-    bad.launch()
-    torch.cuda.synchronize()
     timeout_code = pkg.binding.STATUS_CODE["MHC_STATUS_DEVICE_TIMEOUT"]
+    with pytest.raises(pkg.MhcPreError) as ei:
+        bad.launch(check=True)
+    assert ei.value.status == timeout_code
+    torch.cuda.synchronize()
     assert bad.device_status() == timeout_code
     good.launch()
     torch.cuda.synchronize()
     assert good.device_status() == 0
-    # The status word still holds the first launch's timeout, under its epoch.
+    # The status word still holds the first launch's timeout, under its id.
     assert bad.device_status() == timeout_code
-    check(fetch(good), orc.mhc_pre(x, True, phi, alpha, bias, gamma), x, True, orc)
+    clean = fetch(good)
+    check(clean, orc.mhc_pre(x, True, phi, alpha, bias, gamma), x, True, orc)
+    # The timed-out launch: NaN where it gave up, the clean value elsewhere.
+    poisoned = fetch(bad)
+    hin_bad = poisoned["h_in"]
+    hin_nan = (hin_bad & 0x7F80) == 0x7F80
+    hin_nan &= (hin_bad & 0x007F) != 0
+    assert np.array_equal(hin_bad[~hin_nan], clean["h_in"][~hin_nan])
+    counts = {"h_in": int(hin_nan.sum())}
+    for k in ("h_post", "h_res", "h_pre"):
+        nan = np.isnan(poisoned[k])
+        assert np.array_equal(poisoned[k][~nan], clean[k][~nan]), k
+        counts[k] = int(nan.sum())
+    _say(f"[timeout] NaN elements of the timed-out launch: {counts}")
+    assert counts["h_in"] > 0 and counts["h_pre"] > 0
     good.close()
     bad.close()
+
+
+@pytest.mark.parametrize("force,n,T,D", [("strip", 4, 1000, 7168), ("fused", 4, 600, 1024),
+                                         ("rows", 8, 300, 1024)])
+def test_graph_replays_get_fresh_exchange_epochs(pkg, orc, device, force, n, T, D):
+    """One launch captured into a HIP graph and replayed with new x each time
+    (eager copies and synchronizations between the replays).  The strip
+    kernel's exchange ring reuses its slots within a launch at this size and
+    the fused kernel's records sit at fixed places, so a replay that reused
+    the captured launch's epoch would accept the previous replay's words;
+    every replay must instead match the oracle for its own x and equal an
+    eager launch bit for bit."""
+    import os
+
+    import torch
+
+    K, M = n * D, n * n + 2 * n
+    rng = np.random.default_rng(4100 + T)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.asarray([0.3, -0.2, 0.05], dtype=np.float32)
+    bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    xs = [to_bits(rng.standard_normal((T, n, D)).astype(np.float32) * (1 + 3 * i), True)
+          for i in range(3)]
+    xt, pt, at, bt, gt = to_device(pkg, device, xs[0], True, phi, alpha, bias, gamma)
+    os.environ["MHCPRE_FORCE_PATH"] = force
+    try:
+        op = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True)
+    finally:
+        os.environ.pop("MHCPRE_FORCE_PATH", None)
+    assert op.path == force
+    _say(f"[graph] {force} T={T} n={n} D={D}")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        op.launch(side)  # eager launch before capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        op.launch()
+    torch.cuda.synchronize()
+    for i in (1, 2, 0, 1):
+        src = torch.from_numpy(xs[i].view(np.int16)).to(device).view(torch.bfloat16)
+        xt.copy_(src)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert op.device_status() == 0
+        replayed = fetch(op)
+        check(replayed, orc.mhc_pre(xs[i], True, phi, alpha, bias, gamma), xs[i], True, orc)
+        op.launch()
+        torch.cuda.synchronize()
+        eager = fetch(op)
+        for k in replayed:
+            assert np.array_equal(replayed[k], eager[k]), (i, k)
+    del graph
+    op.close()

@@ -40,6 +40,22 @@ def test_reference_kats(orc):
         assert got == np.float32(w)
 
 
+def test_reference_rint_kats_pin_the_tie_rule(orc):
+    """The reference's round-half-even KATs (audit_group_vec.py:233-234:
+    rint(2.5) = 2, rint(3.5) = 4, rint(-2.5) = -2), applied to the oracle's
+    fp16 / bf16 conversions where one unit is the last place of the format
+    (fp16 in [1024, 2048), bf16 in [128, 256)): a tie must go to the even
+    neighbour, on both signs."""
+    kats = json.loads((GOLDEN / "audit_kats.json").read_text())["rint_half_even"]
+    assert len(kats) == 3
+    for base, enc, dec in ((1024.0, orc.f32_to_f16_bits, orc.f16_bits_to_f32),
+                           (128.0, orc.f32_to_bf16_bits, orc.bf16_bits_to_f32)):
+        for v, want in kats:
+            off = np.float32(base if v >= 0 else -base)
+            got = dec(enc(np.array([off + np.float32(v)], dtype=np.float32)))[0] - off
+            assert got == np.float32(want), (base, v, got, want)
+
+
 def test_f16_exhaustive_against_numpy(orc):
     bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
     want = bits.view(np.float16).astype(np.float32)
