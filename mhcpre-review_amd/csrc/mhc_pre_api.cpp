@@ -507,7 +507,7 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
         if (teamsPerXcd * shape.xcds > p.stripMaxTeams && p.stripMaxTeams < p.fusedTiles) {
             teamsPerXcd = p.stripMaxTeams / shape.xcds;
         }
-        if (teamsPerXcd >= 1 &&
+        if (teamsPerXcd >= 1 && shape.cus <= mhc::kMaxEpochGrid &&
             cached_coresident(executor->stripCoresident, mhc::strip_max_coresident, p, shape.cus) >=
                 shape.cus) {
             mhc::Plan lp = p;
@@ -528,7 +528,7 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
             cached_coresident(executor->fusedCoresident, mhc::fused_max_coresident, p, shape.cus);
         if (coresident >= p.fusedP) {
             mhc::Plan lp = p;
-            lp.fusedTeams = coresident / p.fusedP;
+            lp.fusedTeams = std::min(coresident, mhc::kMaxEpochGrid) / p.fusedP;
             lp.fusedGrid = lp.fusedTeams * p.fusedP;
             err = mhc::launch_fused(lp, workspace, launchId, stream);
             done = true;

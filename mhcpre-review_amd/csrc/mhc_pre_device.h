@@ -169,42 +169,63 @@ __device__ __forceinline__ void split_f16_to_bf16(const float (&f)[8], u32x4_t &
 
 // Exchange epoch of a strip or fused launch, kept in the workspace header.
 // One thread of every workgroup reads the epoch the previous launch on the
-// workspace stored (epoch_load) and the launch uses epoch_next of it, so
+// workspace stored (epoch_load); the launch uses epoch_next of it, so
 // consecutive launches on a workspace, graph replays included, never share an
-// epoch.  After its last read of the header every workgroup reports once
-// (epoch_finish); the report that completes the grid stores the new epoch.
-// The completion word pairs the epoch with a count, so a workspace left with
-// any contents by other use needs no reset.
+// epoch.  Each workgroup records the epoch it uses in its own slot
+// (epoch_mark); one wave of workgroup 0 stores the new epoch at its end, once
+// every workgroup's slot holds it (epoch_publish), so no workgroup can read
+// the advanced value.  No workgroup contends for a word, and a workspace left
+// with any contents by other use needs no reset.
 __device__ __forceinline__ uint32_t epoch_next(uint32_t prev)
 {
     const uint32_t e = prev + 1u;
     return (e == 0u || e == 0xFFFFFFFFu) ? 1u : e;  // 0 and ~0 never tag a word
 }
 
-__device__ __forceinline__ uint32_t epoch_load(void *ws, size_t epochOff)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t header_rsrc(void *ws, size_t off, int bytes)
 {
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(static_cast<char *>(ws) + epochOff, (short)0, 4, 0x00020000);
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 16 /* sc1 */);
+    return __builtin_amdgcn_make_buffer_rsrc(static_cast<char *>(ws) + off, (short)0, bytes, 0x00020000);
 }
 
-__device__ __forceinline__ void epoch_finish(void *ws, size_t epochOff, size_t doneOff, uint32_t epoch,
-                                             uint32_t grid)
+__device__ __forceinline__ uint32_t epoch_load(void *ws, size_t epochOff)
 {
-    uint64_t *done = reinterpret_cast<uint64_t *>(static_cast<char *>(ws) + doneOff);
-    uint32_t *ep = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + epochOff);
-    uint64_t old = __hip_atomic_load(done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (;;) {
-        const uint32_t cnt = (uint32_t)(old >> 32) == epoch ? (uint32_t)old + 1u : 1u;
-        const uint64_t next = ((uint64_t)epoch << 32) | cnt;
-        if (__hip_atomic_compare_exchange_strong(done, &old, next, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT)) {
-            if (cnt == grid) {
-                __hip_atomic_store(ep, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            return;
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(header_rsrc(ws, epochOff, 4), 0, 0, 16 /* sc1 */);
+}
+
+__device__ __forceinline__ void epoch_mark(void *ws, size_t seenOff, uint32_t epoch, int g)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(epoch, header_rsrc(ws, seenOff, 4 * (g + 1)), 4 * g, 0,
+                                          16 /* sc1 */);
+}
+
+// One whole wave: waits (bounded by spinLimit polls) until the slots of all
+// `grid` workgroups hold `epoch`, then stores it as the header's epoch.
+// Returns false if the wait expired (the epoch is stored anyway, so that the
+// next launch cannot reuse it).
+__device__ __forceinline__ bool epoch_publish(void *ws, size_t epochOff, size_t seenOff, uint32_t epoch,
+                                              int grid, uint32_t spinLimit)
+{
+    const int lane = (int)(threadIdx.x & 63);
+    const __amdgpu_buffer_rsrc_t seen = header_rsrc(ws, seenOff, 4 * grid);
+    bool done = false;
+    for (uint32_t spins = 0;; ++spins) {
+        bool ok = true;
+        for (int i = lane; i < grid; i += 64) {
+            ok = ok && (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(seen, 4 * i, 0, 16) == epoch;
         }
+        if (__all(ok)) {
+            done = true;
+            break;
+        }
+        if (spins >= spinLimit) {
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
     }
+    if (lane == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(epoch, header_rsrc(ws, epochOff, 4), 0, 0, 16);
+    }
+    return done;
 }
 
 // Quiet NaN written into the outputs of rows whose exchange wait expired.

@@ -39,7 +39,7 @@
 // no reset of the workspace between launches.  A reader accepts a block only
 // when every word it read carries the expected tag; a block left over from an
 // earlier launch (another epoch) or filled with any constant never does.  The
-// epoch is kept in the workspace header (epoch_load / epoch_finish), so the
+// epoch is kept in the workspace header (epoch_load / mark / publish), so the
 // replays of a captured HIP graph get fresh epochs too.  Every wait is bounded
 // by a spin limit; running out records kDeviceTimeout with the host launch id
 // in the status word instead of hanging, and the values that wait was for are
@@ -258,16 +258,13 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     const int tid = threadIdx.x;
     // Thread 0 reads the epoch the previous launch on this workspace left.
     const uint32_t prevEpoch = tid == 0 ? epoch_load(a.hdr, kWsEpochOff) : 0u;
-    auto finish = [&](uint32_t epoch) {
-        if (tid == 0) {
-            epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch, gridDim.x);
-        }
-    };
     const int P = a.P;
     const int numTeams = a.numTeams;
     const int g = blockIdx.x;
     if (g >= P * numTeams) {
-        finish(epoch_next(prevEpoch));
+        if (tid == 0) {
+            epoch_mark(a.hdr, kWsSeenOff, epoch_next(prevEpoch), g);
+        }
         return;  // spare workgroup: the whole workgroup leaves together
     }
     const int team = g % numTeams;
@@ -294,7 +291,9 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
             u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, xLane + 128 * kp, so, kCpolNt));
     };
     if ((int64_t)team * W >= a.RT) {
-        finish(epoch_next(prevEpoch));
+        if (tid == 0) {
+            epoch_mark(a.hdr, kWsSeenOff, epoch_next(prevEpoch), g);
+        }
         return;  // no row tile for any wave of this workgroup
     }
     if (rt < a.RT) {
@@ -379,6 +378,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     }
     if (tid == 0) {
         epochSh = epoch_next(prevEpoch);
+        epoch_mark(a.hdr, kWsSeenOff, epochSh, g);
     }
     __syncthreads();
 
@@ -707,7 +707,13 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     if (prevTile >= 0) {
         post_res(prevTile, prevInvRms, P, lane);
     }
-    finish(epoch);
+    // Workgroup 0 (team 0, which always has a tile) advances the workspace's
+    // epoch once every workgroup has taken this one.
+    if (g == 0 && wave == 0) {
+        if (!epoch_publish(a.hdr, kWsEpochOff, kWsSeenOff, epoch, (int)gridDim.x, a.spinLimit)) {
+            record_timeout(a, lane);
+        }
+    }
 }
 
 template <int N, int KP, bool kBf16>

@@ -26,12 +26,14 @@ constexpr uint32_t kDeviceTimeout = 0x7107u;
 // exchange epoch of the strip and fused kernels.  The epoch lives in device
 // memory, not in the kernel arguments, so that a launch captured in a HIP
 // graph still gets a fresh epoch on every replay: every workgroup reads the
-// word at kWsEpochOff and uses one more than it; the last workgroup of the
-// grid to finish (counted in the word at kWsDoneOff, which pairs the epoch
-// with the number of finished workgroups) stores the new epoch back.
-constexpr size_t kWsHeaderBytes = 256;
-constexpr size_t kWsEpochOff = 64;   // uint32: epoch of the latest strip / fused launch
-constexpr size_t kWsDoneOff = 128;   // uint64: (epoch << 32) | finished workgroups
+// word at kWsEpochOff, uses one more than it and records the epoch it uses in
+// its own slot of the array at kWsSeenOff; workgroup 0, at its end, stores
+// the new epoch once every slot of the grid holds it (no workgroup reads the
+// word after that).
+constexpr size_t kWsEpochOff = 64;            // uint32: epoch of the latest strip / fused launch
+constexpr size_t kWsSeenOff = 256;            // uint32 [kMaxEpochGrid]: epoch each workgroup uses
+constexpr int kMaxEpochGrid = 2048;           // largest strip / fused grid
+constexpr size_t kWsHeaderBytes = kWsSeenOff + 4 * kMaxEpochGrid;
 
 struct Plan {
     Path path = Path::kSplit;

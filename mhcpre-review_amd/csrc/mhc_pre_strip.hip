@@ -45,7 +45,7 @@
 // position XOR a per-launch epoch, so a word holds the current value exactly
 // when its tag matches: no arrival counter, no release wait, no reset of the
 // workspace between launches.  The epoch is kept in the workspace header
-// (epoch_load / epoch_finish), so replays of a captured HIP graph get fresh
+// (epoch_load / epoch_mark / epoch_publish), so replays of a captured HIP graph get fresh
 // epochs too.  Every wait is bounded by a spin limit; running out records
 // kDeviceTimeout with the host launch id in the status word instead of
 // hanging, and the rows the wave or workgroup could not finish get NaN
@@ -332,6 +332,7 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
     // (prevEpoch), handed to every wave through LDS.
     if (tid == 0) {
         *epochSh = epoch_next(prevEpoch);
+        epoch_mark(a.hdr, kWsSeenOff, *epochSh, blockIdx.x);
     }
     lds_barrier();
     const uint32_t epoch = __builtin_amdgcn_readfirstlane(*epochSh);
@@ -473,9 +474,6 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
         }
         lds_barrier();  // sums / irs are reused by the next tile
     }
-    if (tid == 0) {
-        epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch, gridDim.x);
-    }
 }
 
 template <int N, bool kBf16>
@@ -516,7 +514,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     if (tj >= a.teamsPerXcd) {
         // Spare workgroup: the whole workgroup leaves together.
         if (tid == 0) {
-            epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch_next(prevEpoch), gridDim.x);
+            epoch_mark(a.hdr, kWsSeenOff, epoch_next(prevEpoch), g);
         }
         return;
     }
@@ -561,7 +559,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     }
     if (ntiles == 0) {
         if (tid == 0) {
-            epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch_next(prevEpoch), gridDim.x);
+            epoch_mark(a.hdr, kWsSeenOff, epoch_next(prevEpoch), g);
         }
         return;
     }
@@ -692,6 +690,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     }
     if (tid == 0) {
         epochSh = epoch_next(prevEpoch);
+        epoch_mark(a.hdr, kWsSeenOff, epochSh, g);
     }
     lds_barrier();
     const uint32_t epoch = __builtin_amdgcn_readfirstlane(epochSh);
@@ -978,8 +977,13 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             }
         });
     }
-    if (tid == 0) {
-        epoch_finish(a.hdr, kWsEpochOff, kWsDoneOff, epoch, gridDim.x);
+    // Workgroup 0 (always a slice workgroup of team 0) advances the
+    // workspace's epoch once every workgroup has taken this one.
+    if (g == 0 && w == 0) {
+        if (!epoch_publish(a.hdr, kWsEpochOff, kWsSeenOff, epoch, (int)gridDim.x, spinLimit) &&
+            lane == 0) {
+            st_status(statusW, launchId);
+        }
     }
 }
 

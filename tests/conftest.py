@@ -13,6 +13,19 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD Instinct GPU (gfx950)")
 
 
+def pytest_terminal_summary(terminalreporter):
+    """One line on how much of the hIn tolerance the GPU parity checks used:
+    elements more than 1 ulp from the oracle's hIn (each within the bound the
+    tolerated hPre difference propagates, tests/helpers.py)."""
+    from helpers import HIN_STATS
+
+    if HIN_STATS["checks"]:
+        terminalreporter.write_line(
+            f"hIn vs oracle: {HIN_STATS['beyond']} of {HIN_STATS['elements']} elements beyond "
+            f"1 ulp (max {HIN_STATS['max_ulp']} ulp) over {HIN_STATS['checks']} checks, each "
+            f"within the hPre-propagation bound")
+
+
 @pytest.fixture(scope="session")
 def pkg():
     from __graft_entry__ import load_package

@@ -437,7 +437,10 @@ def test_expired_wait_is_reported_and_cleared(pkg, orc, device, force, n, T, D):
         assert np.array_equal(poisoned[k][~nan], clean[k][~nan]), k
         counts[k] = int(nan.sum())
     _say(f"[timeout] NaN elements of the timed-out launch: {counts}")
-    assert counts["h_in"] > 0 and counts["h_pre"] > 0
+    # Which outputs a given wait covers depends on the path (a fused-path
+    # reducer may find every record at its first poll while the slices'
+    # broadcast waits expire), but some hIn row always waited on hPre.
+    assert counts["h_in"] > 0
     good.close()
     bad.close()
 
