@@ -76,6 +76,8 @@ typedef struct mhcPreExecutor mhcPreExecutor;
                                              the one holding x at phase 1 */
 #define MHC_STATUS_DEVICE_TIMEOUT 8       /* a kernel's bounded inter-workgroup wait expired */
 #define MHC_STATUS_MISALIGNED 9           /* x, hIn, phi, gamma not 16-byte aligned; others not 4 */
+#define MHC_STATUS_SCRATCH_TOO_SMALL 10   /* mhcPreNoAlloc: the executor needs a workspace larger
+                                             than the built-in scratch (64 MiB) */
 
 /*
  * Phase 1.  Replaces aclnnMhcPreGetWorkspaceSize (argument list and meaning
@@ -141,6 +143,22 @@ MHC_API int mhcPreGetWorkspaceSizeWithHPre(const mhcTensor *x, const mhcTensor *
  */
 MHC_API int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor,
            hipStream_t stream);
+
+/*
+ * Phase 2 without a caller workspace.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  As mhcPre, but the
+ * workspace is a fixed 64 MiB array built into the library, one per device,
+ * held until the process ends; the call allocates nothing.  An executor whose
+ * phase-1 workspace size exceeds 64 MiB is rejected with
+ * MHC_STATUS_SCRATCH_TOO_SMALL (every workload up to n=4, D=7168, T=8192 and
+ * n=8, D=8192, T=5472 fits).  All calls on one device share that device's
+ * array: calls that overlap on a device (other streams, other host threads)
+ * race and must be ordered by the caller.  An expired wait between
+ * workgroups shows as NaN in the affected outputs (the status word lives in
+ * the built-in array, which mhcPreQueryDeviceStatus does not read).
+ */
+MHC_API int mhcPreNoAlloc(mhcPreExecutor *executor, hipStream_t stream);
 
 /* Releases an executor (the generated aclnn API frees executors itself). */
 MHC_API int mhcPreExecutorDestroy(mhcPreExecutor *executor);

@@ -29,6 +29,7 @@ STATUS = {
     7: "MHC_STATUS_DEVICE_MISMATCH",
     8: "MHC_STATUS_DEVICE_TIMEOUT",
     9: "MHC_STATUS_MISALIGNED",
+    10: "MHC_STATUS_SCRATCH_TOO_SMALL",
 }
 STATUS_CODE = {v: k for k, v in STATUS.items()}
 
@@ -91,6 +92,8 @@ def load_library() -> ctypes.CDLL:
     lib.mhcPreStatusString.restype = ctypes.c_char_p
     lib.mhcPreExecutorPath.argtypes = [exe, P(ctypes.c_char_p)]
     lib.mhcPreExecutorPath.restype = ctypes.c_int
+    lib.mhcPreNoAlloc.argtypes = [exe, ctypes.c_void_p]
+    lib.mhcPreNoAlloc.restype = ctypes.c_int
     _LIB = lib
     return lib
 
@@ -231,6 +234,20 @@ class MhcPreOp:
             raise MhcPreError("mhcPre", st)
         if check:
             self.check(stream)
+
+    def launch_no_alloc(self, stream=None) -> None:
+        """Enqueue one launch through mhcPreNoAlloc: the library's built-in
+        per-device scratch array is the workspace (this object's workspace
+        tensor is not used) and the call allocates nothing."""
+        import torch
+
+        if torch.cuda.current_device() != self._dev_index:
+            with torch.cuda.device(self._dev_index):
+                st = self.lib.mhcPreNoAlloc(self.executor, ctypes.c_void_p(_stream_handle(stream)))
+        else:
+            st = self.lib.mhcPreNoAlloc(self.executor, ctypes.c_void_p(_stream_handle(stream)))
+        if st != 0:
+            raise MhcPreError("mhcPreNoAlloc", st)
 
     def check(self, stream=None) -> None:
         """Synchronize ``stream`` and raise if this executor's latest launch

@@ -605,6 +605,29 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
     return launch_on(workspace, executor, stream);
 }
 
+int mhcPreNoAlloc(mhcPreExecutor *executor, hipStream_t stream)
+{
+    if (executor == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    // The built-in workspace has a fixed size: larger plans are rejected
+    // before any HIP call.
+    if (executor->plan.wsTotal > mhc::kScratchBytes) {
+        return MHC_STATUS_SCRATCH_TOO_SMALL;
+    }
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess) {
+        (void)hipGetLastError();
+        return MHC_STATUS_HIP_ERROR;
+    }
+    void *ws = nullptr;
+    if (mhc::scratch_address(device, &ws) != hipSuccess) {
+        (void)hipGetLastError();
+        return MHC_STATUS_HIP_ERROR;
+    }
+    return launch_on(ws, executor, stream);
+}
+
 int mhcPreExecutorDestroy(mhcPreExecutor *executor)
 {
     if (executor == nullptr) {
@@ -660,6 +683,8 @@ const char *mhcPreStatusString(int status)
         return "device timeout";
     case MHC_STATUS_MISALIGNED:
         return "misaligned device pointer";
+    case MHC_STATUS_SCRATCH_TOO_SMALL:
+        return "workspace larger than the built-in scratch";
     default:
         return "unknown status";
     }

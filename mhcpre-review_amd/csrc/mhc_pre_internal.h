@@ -118,6 +118,12 @@ struct Plan {
     float *hPre = nullptr;
 };
 
+// Built-in workspace of mhcPreNoAlloc (mhc_pre_noalloc.hip): kScratchBytes
+// per device, in the library's device code object.  scratch_address gives the
+// current device's copy (the caller makes `device` current).
+constexpr size_t kScratchBytes = size_t{64} << 20;
+hipError_t scratch_address(int device, void **ptr);
+
 // Kernel launchers (mhc_pre_kernels.hip).  Each returns the first HIP error.
 hipError_t launch_split(const Plan &plan, void *workspace, hipStream_t stream);
 // launchId: host-side id of the launch, written with kDeviceTimeout into the

@@ -257,3 +257,26 @@ def test_forced_paths(pkg, lib):
     assert _path(pkg, lib, _descs(pkg, S=64, n=4, D=7168), env="strip") == "strip"
     # A path the shape cannot take is ignored.
     assert _path(pkg, lib, _descs(pkg, S=16, n=6, D=48), env="rows") == "split"
+
+
+def test_no_alloc_rejects_workspaces_beyond_the_builtin_scratch(pkg, lib):
+    """mhcPreNoAlloc checks the executor's workspace size against its 64 MiB
+    built-in array before any HIP call: a plan that needs more (the fused
+    layout of 131072 rows at n=4, D=1024: 8192 row tiles x 4 slices of
+    exchange records) is rejected with MHC_STATUS_SCRATCH_TOO_SMALL, and a
+    NULL executor with MHC_STATUS_NULL_ARGUMENT."""
+    T, n, D = 131072, 4, 1024
+    d = _descs(pkg, B=1, S=T, n=n, D=D)
+    mk = lambda v: None if v is None else ctypes.byref(pkg.make_tensor(*v))
+    ws, exe = ctypes.c_uint64(0), ctypes.c_void_p(None)
+    st = lib.mhcPreGetWorkspaceSize(mk(d["x"]), mk(d["phi"]), mk(d["alpha"]), mk(d["bias"]),
+                                    mk(d["gamma"]), ctypes.c_float(1e-6), ctypes.c_float(1e-6),
+                                    mk(d["hIn"]), mk(d["hPost"]), mk(d["hRes"]),
+                                    ctypes.byref(ws), ctypes.byref(exe))
+    assert st == 0 and ws.value > 64 << 20
+    try:
+        assert lib.mhcPreNoAlloc(exe, None) == code(pkg, "MHC_STATUS_SCRATCH_TOO_SMALL")
+    finally:
+        lib.mhcPreExecutorDestroy(exe)
+    assert lib.mhcPreNoAlloc(None, None) == code(pkg, "MHC_STATUS_NULL_ARGUMENT")
+    assert lib.mhcPreStatusString(code(pkg, "MHC_STATUS_SCRATCH_TOO_SMALL")) != b"unknown status"
