@@ -145,6 +145,57 @@ MHC_API int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *exec
            hipStream_t stream);
 
 /*
+ * Prepared weights.  Extension; the reference rebuilds its GEMM operand from
+ * phi and gamma on every launch (the gamma product in PreprocessRows and the
+ * phi read of ProjectWithCube, code/op_kernel/mhc_pre.cpp:466-468,535, with
+ * the per-call tiling of code/op_host/mhc_pre.cpp:159-177).  For weights that
+ * stay fixed over many launches, mhcPrePrepareWeights computes
+ * B = gamma (.) phi once, split into bf16 hi + lo MFMA fragments, into a
+ * caller-owned device buffer; executors created from it
+ * (mhcPreGetWorkspaceSizePrepared) copy or read those fragments instead of
+ * building them from phi and gamma on every launch.  Results are bit-identical
+ * to executors built from phi and gamma.
+ *
+ * `n` is the stream count (4, 6 or 8; M = n*n + 2n); phi is fp32 with K*M
+ * elements (memory [M][K], as for phase 1), gamma fp32 with K elements or
+ * NULL / zero elements for none.  The buffer must hold
+ * mhcPrePrepareWeightsSize bytes (K * 2M * 2), be 256-byte aligned and live on
+ * the current device.  The preparation is enqueued on `stream`; launches on
+ * other streams must be ordered after it by the caller.
+ *
+ * `version` is the caller's key for the weights the buffer holds (for example
+ * an update counter); mhcPreWeightsVersion returns it.  Preparing again into
+ * the same buffer (same shapes) updates, from their next launch on, every
+ * executor created from that buffer; the buffer must outlive them, the
+ * weights object need not.
+ */
+typedef struct mhcPreWeights mhcPreWeights;
+
+MHC_API int mhcPrePrepareWeightsSize(const mhcTensor *phi, const mhcTensor *gamma, int32_t n,
+                                     uint64_t *bytes);
+
+MHC_API int mhcPrePrepareWeights(const mhcTensor *phi, const mhcTensor *gamma, int32_t n,
+                                 void *buffer, uint64_t bytes, uint64_t version,
+                                 hipStream_t stream, mhcPreWeights **weights);
+
+MHC_API int mhcPreWeightsVersion(const mhcPreWeights *weights, uint64_t *version);
+
+MHC_API int mhcPreWeightsDestroy(mhcPreWeights *weights);
+
+/*
+ * Phase 1 from prepared weights: as mhcPreGetWorkspaceSizeWithHPre with phi
+ * and gamma replaced by `weights` (x's n must be the prepared n and its n*D
+ * the prepared K; MHC_STATUS_INVALID_SHAPE otherwise).  hPre may be NULL.
+ * The executor reads the weights' buffer at every launch.
+ */
+MHC_API int mhcPreGetWorkspaceSizePrepared(const mhcTensor *x, const mhcPreWeights *weights,
+                                           const mhcTensor *alpha, const mhcTensor *bias,
+                                           float normEps, float hcEps, const mhcTensor *hIn,
+                                           const mhcTensor *hPost, const mhcTensor *hRes,
+                                           const mhcTensor *hPre, uint64_t *workspaceSize,
+                                           mhcPreExecutor **executor);
+
+/*
  * Phase 2 without a caller workspace.  No counterpart in the reference: for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  As mhcPre, but the

@@ -17,6 +17,7 @@ from .binding import (  # noqa: F401
     STATUS,
     MhcPreError,
     MhcPreOp,
+    MhcPreWeights,
     MhcTensor,
     exported_symbols,
     library_path,

@@ -94,6 +94,19 @@ def load_library() -> ctypes.CDLL:
     lib.mhcPreExecutorPath.restype = ctypes.c_int
     lib.mhcPreNoAlloc.argtypes = [exe, ctypes.c_void_p]
     lib.mhcPreNoAlloc.restype = ctypes.c_int
+    w = ctypes.c_void_p
+    lib.mhcPrePrepareWeightsSize.argtypes = [T, T, ctypes.c_int32, P(ctypes.c_uint64)]
+    lib.mhcPrePrepareWeightsSize.restype = ctypes.c_int
+    lib.mhcPrePrepareWeights.argtypes = [T, T, ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint64,
+                                         ctypes.c_uint64, ctypes.c_void_p, P(w)]
+    lib.mhcPrePrepareWeights.restype = ctypes.c_int
+    lib.mhcPreWeightsVersion.argtypes = [w, P(ctypes.c_uint64)]
+    lib.mhcPreWeightsVersion.restype = ctypes.c_int
+    lib.mhcPreWeightsDestroy.argtypes = [w]
+    lib.mhcPreWeightsDestroy.restype = ctypes.c_int
+    lib.mhcPreGetWorkspaceSizePrepared.argtypes = [T, w, T, T, ctypes.c_float, ctypes.c_float,
+                                                   T, T, T, T, P(ctypes.c_uint64), P(exe)]
+    lib.mhcPreGetWorkspaceSizePrepared.restype = ctypes.c_int
     _LIB = lib
     return lib
 
@@ -139,18 +152,85 @@ def _stream_handle(stream) -> int:
     return int(stream.cuda_stream)
 
 
+class MhcPreWeights:
+    """Prepared B operand (mhcPrePrepareWeights): gamma (.) phi as bf16 hi + lo
+    MFMA fragments in a device buffer this object owns (a torch tensor).
+    ``prepare`` recomputes it in place from new weights of the same shapes and
+    records the new version; executors created from this object read the new
+    contents from their next launch on."""
+
+    def __init__(self, phi, gamma, n: int, version: int = 0, stream=None):
+        import torch
+
+        self.lib = load_library()
+        self.n = int(n)
+        self.handle = ctypes.c_void_p(None)
+        size = ctypes.c_uint64(0)
+        pd = tensor_desc(phi)
+        gd = tensor_desc(gamma) if gamma is not None else None
+        st = self.lib.mhcPrePrepareWeightsSize(ctypes.byref(pd),
+                                               ctypes.byref(gd) if gd is not None else None,
+                                               ctypes.c_int32(self.n), ctypes.byref(size))
+        if st != 0:
+            raise MhcPreError("mhcPrePrepareWeightsSize", st)
+        self.bytes = int(size.value)
+        self.buffer = torch.empty(max(self.bytes, 256), dtype=torch.uint8, device=phi.device)
+        self.prepare(phi, gamma, version, stream)
+
+    def prepare(self, phi, gamma, version: int, stream=None) -> None:
+        import torch
+
+        pd = tensor_desc(phi)
+        gd = tensor_desc(gamma) if gamma is not None else None
+        handle = ctypes.c_void_p(None)
+        with torch.cuda.device(self.buffer.device):
+            st = self.lib.mhcPrePrepareWeights(
+                ctypes.byref(pd), ctypes.byref(gd) if gd is not None else None,
+                ctypes.c_int32(self.n), ctypes.c_void_p(self.buffer.data_ptr()),
+                ctypes.c_uint64(self.bytes), ctypes.c_uint64(int(version)),
+                ctypes.c_void_p(_stream_handle(stream)), ctypes.byref(handle))
+        if st != 0:
+            raise MhcPreError("mhcPrePrepareWeights", st)
+        self.close()
+        self.handle = handle
+        # phi and gamma are read by the enqueued preparation: keep them alive
+        # until it has run (the caller's stream order covers later launches).
+        self._inputs = (phi, gamma)
+
+    @property
+    def version(self) -> int:
+        v = ctypes.c_uint64(0)
+        st = self.lib.mhcPreWeightsVersion(self.handle, ctypes.byref(v))
+        if st != 0:
+            raise MhcPreError("mhcPreWeightsVersion", st)
+        return int(v.value)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.lib.mhcPreWeightsDestroy(self.handle)
+            self.handle = ctypes.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class MhcPreOp:
     """One executor plus its workspace: phase 1 at construction, phase 2 per launch.
 
     Outputs not given are allocated on x's device.  ``h_pre=True`` allocates the
     optional hPre output (extension entry point).  phi is passed with its
     declared shape [n*D, M] unless ``phi_dims`` overrides it; its memory is
-    read as [M][K] either way.
+    read as [M][K] either way.  With ``weights`` (a :class:`MhcPreWeights`)
+    the executor comes from mhcPreGetWorkspaceSizePrepared, and phi and gamma
+    must be None.
     """
 
     def __init__(self, x, phi, alpha, bias, gamma=None, norm_eps: float = 1e-6,
                  hc_eps: float = 1e-6, h_in=None, h_post=None, h_res=None, h_pre=None,
-                 phi_dims=None, workspace=None):
+                 phi_dims=None, workspace=None, weights=None):
         import torch
 
         self.lib = load_library()
@@ -169,25 +249,35 @@ class MhcPreOp:
             h_pre = torch.empty(lead + [n], dtype=torch.float32, device=dev)
         self.h_pre = h_pre if h_pre is not False else None
         # Keep the inputs alive as long as the executor that binds them.
-        self._keep = (x, phi, alpha, bias, gamma)
-        descs = [tensor_desc(x), tensor_desc(phi, phi_dims), tensor_desc(alpha),
-                 tensor_desc(bias)]
-        g = tensor_desc(gamma) if gamma is not None else None
+        self._keep = (x, phi, alpha, bias, gamma, weights)
         outs = [tensor_desc(self.h_in), tensor_desc(self.h_post), tensor_desc(self.h_res)]
         ws = ctypes.c_uint64(0)
         exe = ctypes.c_void_p(None)
-        gp = ctypes.byref(g) if g is not None else None
-        if self.h_pre is not None:
-            hp = tensor_desc(self.h_pre)
-            st = self.lib.mhcPreGetWorkspaceSizeWithHPre(
-                *[ctypes.byref(d) for d in descs], gp, ctypes.c_float(norm_eps),
-                ctypes.c_float(hc_eps), *[ctypes.byref(d) for d in outs], ctypes.byref(hp),
-                ctypes.byref(ws), ctypes.byref(exe))
+        hp = tensor_desc(self.h_pre) if self.h_pre is not None else None
+        hpp = ctypes.byref(hp) if hp is not None else None
+        if weights is not None:
+            if phi is not None or gamma is not None:
+                raise ValueError("with prepared weights, phi and gamma must be None")
+            xd, ad, bd = tensor_desc(x), tensor_desc(alpha), tensor_desc(bias)
+            st = self.lib.mhcPreGetWorkspaceSizePrepared(
+                ctypes.byref(xd), weights.handle, ctypes.byref(ad), ctypes.byref(bd),
+                ctypes.c_float(norm_eps), ctypes.c_float(hc_eps), *[ctypes.byref(d) for d in outs],
+                hpp, ctypes.byref(ws), ctypes.byref(exe))
         else:
-            st = self.lib.mhcPreGetWorkspaceSize(
-                *[ctypes.byref(d) for d in descs], gp, ctypes.c_float(norm_eps),
-                ctypes.c_float(hc_eps), *[ctypes.byref(d) for d in outs], ctypes.byref(ws),
-                ctypes.byref(exe))
+            descs = [tensor_desc(x), tensor_desc(phi, phi_dims), tensor_desc(alpha),
+                     tensor_desc(bias)]
+            g = tensor_desc(gamma) if gamma is not None else None
+            gp = ctypes.byref(g) if g is not None else None
+            if hp is not None:
+                st = self.lib.mhcPreGetWorkspaceSizeWithHPre(
+                    *[ctypes.byref(d) for d in descs], gp, ctypes.c_float(norm_eps),
+                    ctypes.c_float(hc_eps), *[ctypes.byref(d) for d in outs], hpp,
+                    ctypes.byref(ws), ctypes.byref(exe))
+            else:
+                st = self.lib.mhcPreGetWorkspaceSize(
+                    *[ctypes.byref(d) for d in descs], gp, ctypes.c_float(norm_eps),
+                    ctypes.c_float(hc_eps), *[ctypes.byref(d) for d in outs], ctypes.byref(ws),
+                    ctypes.byref(exe))
         if st != 0:
             raise MhcPreError("mhcPreGetWorkspaceSize", st)
         self.executor = exe

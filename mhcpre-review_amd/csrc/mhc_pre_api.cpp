@@ -23,6 +23,17 @@
 #include <mutex>
 #include <new>
 
+// Prepared weights: B = gamma (.) phi as bf16 hi + lo MFMA fragments in a
+// caller-owned device buffer (layout of mhc::launch_prepare_b).
+struct mhcPreWeights {
+    int n = 0;
+    int M = 0;
+    int64_t K = 0;
+    void *buffer = nullptr;
+    uint64_t version = 0;
+    int device = -1;  // device holding the buffer (-1: unknown)
+};
+
 struct mhcPreExecutor {
     mhc::Plan plan;
     // Device that holds x (-1: the runtime could not tell, e.g. no device is
@@ -427,6 +438,39 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
 
 void prime_coresident(mhcPreExecutor *ex);
 
+// Shape and type rules of weights to prepare: those phase 1 applies to phi
+// and gamma (element counts: phi K*M, gamma K or none), with K taken from
+// phi's element count and D = K / n a multiple of 16.
+int weights_shape(const mhcTensor *phi, const mhcTensor *gamma, int32_t n, int &M, int64_t &K,
+                  bool &hasGamma)
+{
+    if (phi == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    if (n != 4 && n != 6 && n != 8) {
+        return MHC_STATUS_UNSUPPORTED_SHAPE;
+    }
+    M = n * n + 2 * n;
+    hasGamma = gamma != nullptr && numel(*gamma) > 0 && gamma->ndim > 0;
+    if (phi->dtype != MHC_DTYPE_FLOAT || (hasGamma && gamma->dtype != MHC_DTYPE_FLOAT)) {
+        return MHC_STATUS_INVALID_DTYPE;
+    }
+    const int64_t count = numel(*phi);
+    if (!dims_positive(*phi) || count <= 0 || count % M != 0) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    K = count / M;
+    if (K % n != 0 || (K / n) % 16 != 0 || K / n > kMaxWidth) {
+        return MHC_STATUS_UNSUPPORTED_SHAPE;
+    }
+    if (hasGamma && (!dims_positive(*gamma) || numel(*gamma) != K)) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    return MHC_STATUS_SUCCESS;
+}
+
+uint64_t prepared_bytes(int M, int64_t K) { return static_cast<uint64_t>(K) * static_cast<uint64_t>(2 * M) * 2; }
+
 int get_workspace(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alpha,
                   const mhcTensor *bias, const mhcTensor *gamma, float normEps, float hcEps,
                   const mhcTensor *hIn, const mhcTensor *hPost, const mhcTensor *hRes,
@@ -603,6 +647,148 @@ int mhcPre(void *workspace, uint64_t workspaceSize, mhcPreExecutor *executor, hi
         return MHC_STATUS_WORKSPACE_TOO_SMALL;
     }
     return launch_on(workspace, executor, stream);
+}
+
+int mhcPrePrepareWeightsSize(const mhcTensor *phi, const mhcTensor *gamma, int32_t n,
+                             uint64_t *bytes)
+{
+    if (bytes == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    int M = 0;
+    int64_t K = 0;
+    bool hasGamma = false;
+    const int st = weights_shape(phi, gamma, n, M, K, hasGamma);
+    if (st != MHC_STATUS_SUCCESS) {
+        return st;
+    }
+    *bytes = prepared_bytes(M, K);
+    return MHC_STATUS_SUCCESS;
+}
+
+int mhcPrePrepareWeights(const mhcTensor *phi, const mhcTensor *gamma, int32_t n, void *buffer,
+                         uint64_t bytes, uint64_t version, hipStream_t stream,
+                         mhcPreWeights **weights)
+{
+    if (weights == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    *weights = nullptr;
+    int M = 0;
+    int64_t K = 0;
+    bool hasGamma = false;
+    const int st = weights_shape(phi, gamma, n, M, K, hasGamma);
+    if (st != MHC_STATUS_SUCCESS) {
+        return st;
+    }
+    if (buffer == nullptr || phi->data == nullptr || (hasGamma && gamma->data == nullptr)) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    if (bytes < prepared_bytes(M, K)) {
+        return MHC_STATUS_WORKSPACE_TOO_SMALL;
+    }
+    if (!aligned(buffer, 256) || !aligned(phi->data, 16) || (hasGamma && !aligned(gamma->data, 16))) {
+        return MHC_STATUS_MISALIGNED;
+    }
+    // The preparation runs on the current device, which must hold the buffer.
+    const int device = device_of(buffer);
+    if (device >= 0) {
+        int current = -1;
+        if (hipGetDevice(&current) != hipSuccess) {
+            (void)hipGetLastError();
+            return MHC_STATUS_HIP_ERROR;
+        }
+        if (current != device) {
+            return MHC_STATUS_DEVICE_MISMATCH;
+        }
+    }
+    mhcPreWeights *w = new (std::nothrow) mhcPreWeights;
+    if (w == nullptr) {
+        return MHC_STATUS_HIP_ERROR;
+    }
+    // The launch's status is read back with hipGetLastError: first clear an
+    // error an earlier call of the process may have left there.
+    (void)hipGetLastError();
+    if (mhc::launch_prepare_b(n, static_cast<const float *>(phi->data),
+                              hasGamma ? static_cast<const float *>(gamma->data) : nullptr, buffer, K,
+                              stream) != hipSuccess) {
+        (void)hipGetLastError();
+        delete w;
+        return MHC_STATUS_HIP_ERROR;
+    }
+    w->n = n;
+    w->M = M;
+    w->K = K;
+    w->buffer = buffer;
+    w->version = version;
+    w->device = device;
+    *weights = w;
+    return MHC_STATUS_SUCCESS;
+}
+
+int mhcPreWeightsVersion(const mhcPreWeights *weights, uint64_t *version)
+{
+    if (weights == nullptr || version == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    *version = weights->version;
+    return MHC_STATUS_SUCCESS;
+}
+
+int mhcPreWeightsDestroy(mhcPreWeights *weights)
+{
+    if (weights == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    delete weights;
+    return MHC_STATUS_SUCCESS;
+}
+
+int mhcPreGetWorkspaceSizePrepared(const mhcTensor *x, const mhcPreWeights *weights,
+                                   const mhcTensor *alpha, const mhcTensor *bias, float normEps,
+                                   float hcEps, const mhcTensor *hIn, const mhcTensor *hPost,
+                                   const mhcTensor *hRes, const mhcTensor *hPre,
+                                   uint64_t *workspaceSize, mhcPreExecutor **executor)
+{
+    if (weights == nullptr || workspaceSize == nullptr || executor == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    *executor = nullptr;
+    // phi stands in for the prepared buffer in phase 1's checks (element
+    // count K*M, fp32, aligned); gamma is folded into the prepared B.
+    mhcTensor phiD{};
+    phiD.data = weights->buffer;
+    phiD.dtype = MHC_DTYPE_FLOAT;
+    phiD.ndim = 2;
+    phiD.dims[0] = weights->K;
+    phiD.dims[1] = weights->M;
+    mhc::Plan plan;
+    const int st = validate_and_plan(x, &phiD, alpha, bias, nullptr, normEps, hcEps, hIn, hPost, hRes,
+                                     hPre, plan);
+    if (st != MHC_STATUS_SUCCESS) {
+        return st;
+    }
+    if (plan.n != weights->n || plan.K != weights->K) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    const int device = device_of(plan.x);
+    if (device >= 0 && weights->device >= 0 && device != weights->device) {
+        return MHC_STATUS_DEVICE_MISMATCH;
+    }
+    plan.bprep = weights->buffer;
+    plan.phi = nullptr;
+    plan.gamma = nullptr;
+    plan.hasGamma = false;
+    mhcPreExecutor *ex = new (std::nothrow) mhcPreExecutor;
+    if (ex == nullptr) {
+        return MHC_STATUS_HIP_ERROR;
+    }
+    ex->plan = plan;
+    ex->device = device;
+    prime_coresident(ex);
+    *workspaceSize = plan.wsTotal;
+    *executor = ex;
+    return MHC_STATUS_SUCCESS;
 }
 
 int mhcPreNoAlloc(mhcPreExecutor *executor, hipStream_t stream)

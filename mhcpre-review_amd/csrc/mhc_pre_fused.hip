@@ -68,6 +68,7 @@ struct FusedArgs {
     const uint16_t *x;
     const float *phi;
     const float *gamma;
+    const u32x4_t *bprep;  // prepared B fragments [K/32][NT][64] (kPrep only)
     const float *alpha;
     const float *bias;
     uint16_t *hIn;
@@ -239,7 +240,7 @@ __device__ __forceinline__ void record_timeout(const FusedArgs &a, int lane)
     }
 }
 
-template <int N, int KP, bool kBf16>
+template <int N, int KP, bool kBf16, bool kPrep>
 __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
 {
     using S = Shape<N>;
@@ -318,60 +319,72 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     // B[k = s*D + d0 + 32ks + 8(l/16) + e][slot 16ct + l%16], e = 0..7.  A
     // thread builds all NT column tiles of one (s, ks, lane) item, so it reads
     // the item's gamma once; two items' loads are in flight together.
-    constexpr int ITEMS = N * KS * 64;
-    for (int it0 = tid; it0 < ITEMS; it0 += 2 * W * 64) {
-        f32x4_t ph[2][NT][2];
-        f32x4_t gm[2][2];
+    if constexpr (kPrep) {
+        // Prepared weights: the fragments already have this layout; k-step ks
+        // of stream s is the prepared k-step (s D + d0 + 32 ks) / 32.
+        constexpr int FR = N * KS * NT * 64;
+        for (int f = tid; f < FR; f += W * 64) {
+            const int sk = f / (NT * 64);
+            const int ct = (f / 64) % NT;
+            const int64_t gks = ((sk / KS) * a.D + d0 + 32 * (sk % KS)) / 32;
+            bl[f] = a.bprep[(gks * NT + ct) * 64 + (f & 63)];
+        }
+    } else {
+        constexpr int ITEMS = N * KS * 64;
+        for (int it0 = tid; it0 < ITEMS; it0 += 2 * W * 64) {
+            f32x4_t ph[2][NT][2];
+            f32x4_t gm[2][2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int it = it0 + h * W * 64;
-            if (it < ITEMS) {
-                const int fl = it & 63;
-                const int sk = it >> 6;
-                const int64_t k0 =
-                    (sk / KS) * a.D + d0 + 32 * (sk % KS) + 8 * (fl >> 4);
+            for (int h = 0; h < 2; ++h) {
+                const int it = it0 + h * W * 64;
+                if (it < ITEMS) {
+                    const int fl = it & 63;
+                    const int sk = it >> 6;
+                    const int64_t k0 =
+                        (sk / KS) * a.D + d0 + 32 * (sk % KS) + 8 * (fl >> 4);
 #pragma unroll
-                for (int ct = 0; ct < NT; ++ct) {
-                    bool lo;
-                    int j;
-                    CL::slot(16 * ct + (fl & 15), lo, j);
-                    const f32x4_t *src =
-                        reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + k0);
-                    ph[h][ct][0] = src[0];
-                    ph[h][ct][1] = src[1];
-                }
-                if (a.gamma != nullptr) {
-                    const f32x4_t *gs = reinterpret_cast<const f32x4_t *>(a.gamma + k0);
-                    gm[h][0] = gs[0];
-                    gm[h][1] = gs[1];
-                } else {
-                    gm[h][0] = f32x4_t{1.f, 1.f, 1.f, 1.f};
-                    gm[h][1] = f32x4_t{1.f, 1.f, 1.f, 1.f};
+                    for (int ct = 0; ct < NT; ++ct) {
+                        bool lo;
+                        int j;
+                        CL::slot(16 * ct + (fl & 15), lo, j);
+                        const f32x4_t *src =
+                            reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + k0);
+                        ph[h][ct][0] = src[0];
+                        ph[h][ct][1] = src[1];
+                    }
+                    if (a.gamma != nullptr) {
+                        const f32x4_t *gs = reinterpret_cast<const f32x4_t *>(a.gamma + k0);
+                        gm[h][0] = gs[0];
+                        gm[h][1] = gs[1];
+                    } else {
+                        gm[h][0] = f32x4_t{1.f, 1.f, 1.f, 1.f};
+                        gm[h][1] = f32x4_t{1.f, 1.f, 1.f, 1.f};
+                    }
                 }
             }
-        }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int it = it0 + h * W * 64;
-            if (it < ITEMS) {
-                const int fl = it & 63;
-                const int sk = it >> 6;
+            for (int h = 0; h < 2; ++h) {
+                const int it = it0 + h * W * 64;
+                if (it < ITEMS) {
+                    const int fl = it & 63;
+                    const int sk = it >> 6;
 #pragma unroll
-                for (int ct = 0; ct < NT; ++ct) {
-                    bool lo;
-                    int j;
-                    CL::slot(16 * ct + (fl & 15), lo, j);
-                    float out[8];
+                    for (int ct = 0; ct < NT; ++ct) {
+                        bool lo;
+                        int j;
+                        CL::slot(16 * ct + (fl & 15), lo, j);
+                        float out[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        float b = ph[h][ct][e >> 2][e & 3];
-                        if (a.gamma != nullptr) {
-                            b = b * gm[h][e >> 2][e & 3];
+                        for (int e = 0; e < 8; ++e) {
+                            float b = ph[h][ct][e >> 2][e & 3];
+                            if (a.gamma != nullptr) {
+                                b = b * gm[h][e >> 2][e & 3];
+                            }
+                            const float hi = bf16_bits_to_f32(f32_to_bf16_bits(b));
+                            out[e] = lo ? (b - hi) : hi;
                         }
-                        const float hi = bf16_bits_to_f32(f32_to_bf16_bits(b));
-                        out[e] = lo ? (b - hi) : hi;
+                        bl[(sk * NT + ct) * 64 + fl] = pack8_bf16(out);
                     }
-                    bl[(sk * NT + ct) * 64 + fl] = pack8_bf16(out);
                 }
             }
         }
@@ -716,7 +729,7 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
     }
 }
 
-template <int N, int KP, bool kBf16>
+template <int N, int KP, bool kBf16, bool kPrep>
 size_t fused_lds_bytes()
 {
     return (size_t)N * 2 * KP * Shape<N>::NT * 64 * sizeof(u32x4_t) +
@@ -724,38 +737,38 @@ size_t fused_lds_bytes()
            (size_t)kFusedWaves * Rec<N>::WORDS * sizeof(uint64_t);
 }
 
-template <int N, int KP, bool kBf16>
+template <int N, int KP, bool kBf16, bool kPrep>
 hipError_t fused_prepare_attr()
 {
     static std::once_flag once;
     static hipError_t err = hipSuccess;
     std::call_once(once, [] {
-        err = hipFuncSetAttribute(reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16>),
+        err = hipFuncSetAttribute(reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16, kPrep>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)fused_lds_bytes<N, KP, kBf16>());
+                                  (int)fused_lds_bytes<N, KP, kBf16, kPrep>());
     });
     return err;
 }
 
-template <int N, int KP, bool kBf16>
+template <int N, int KP, bool kBf16, bool kPrep>
 int fused_coresident_t(int numCUs)
 {
-    if (fused_prepare_attr<N, KP, kBf16>() != hipSuccess) {
+    if (fused_prepare_attr<N, KP, kBf16, kPrep>() != hipSuccess) {
         return -1;
     }
     int perCU = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &perCU, reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16>),
-            kFusedWaves * 64, fused_lds_bytes<N, KP, kBf16>()) != hipSuccess) {
+            &perCU, reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16, kPrep>),
+            kFusedWaves * 64, fused_lds_bytes<N, KP, kBf16, kPrep>()) != hipSuccess) {
         return -1;
     }
     return perCU * numCUs;
 }
 
-template <int N, int KP, bool kBf16>
+template <int N, int KP, bool kBf16, bool kPrep>
 hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t launchId, hipStream_t stream)
 {
-    hipError_t err = fused_prepare_attr<N, KP, kBf16>();
+    hipError_t err = fused_prepare_attr<N, KP, kBf16, kPrep>();
     if (err != hipSuccess) {
         return err;
     }
@@ -764,6 +777,7 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t launchId, hip
     a.x = static_cast<const uint16_t *>(p.x);
     a.phi = p.phi;
     a.gamma = p.hasGamma ? p.gamma : nullptr;
+    a.bprep = static_cast<const u32x4_t *>(p.bprep);
     a.alpha = p.alpha;
     a.bias = p.bias;
     a.hIn = static_cast<uint16_t *>(p.hIn);
@@ -786,31 +800,38 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t launchId, hip
     a.launchId = launchId;
     a.spinLimit = p.spinLimit;
 
-    const unsigned lds = (unsigned)fused_lds_bytes<N, KP, kBf16>();
+    const unsigned lds = (unsigned)fused_lds_bytes<N, KP, kBf16, kPrep>();
     if (!p.fusedCooperative) {
-        hipLaunchKernelGGL((fused_kernel<N, KP, kBf16>), dim3((unsigned)p.fusedGrid),
+        hipLaunchKernelGGL((fused_kernel<N, KP, kBf16, kPrep>), dim3((unsigned)p.fusedGrid),
                            dim3(kFusedWaves * 64), lds, stream, a);
         return hipGetLastError();
     }
     void *args[] = {&a};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16>),
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&fused_kernel<N, KP, kBf16, kPrep>),
                                       dim3((unsigned)p.fusedGrid), dim3(kFusedWaves * 64), args,
                                       lds, stream);
 }
 
 }  // namespace
 
-// Fused-path instantiations: n = 4 with KP in {4, 2, 1} (DW = 256, 128, 64).
-#define MHC_FUSED_DISPATCH(FN, ...)                                            \
+// Fused-path instantiations: n = 4 with KP in {4, 2, 1} (DW = 256, 128, 64),
+// B built from phi and gamma or copied from prepared weights.
+#define MHC_FUSED_DISPATCH_P(FN, PREP, ...)                                    \
     switch (p.fusedDw / 64) {                                                  \
     case 4:                                                                    \
-        return p.isBf16 ? FN<4, 4, true>(__VA_ARGS__) : FN<4, 4, false>(__VA_ARGS__); \
+        return p.isBf16 ? FN<4, 4, true, PREP>(__VA_ARGS__) : FN<4, 4, false, PREP>(__VA_ARGS__); \
     case 2:                                                                    \
-        return p.isBf16 ? FN<4, 2, true>(__VA_ARGS__) : FN<4, 2, false>(__VA_ARGS__); \
+        return p.isBf16 ? FN<4, 2, true, PREP>(__VA_ARGS__) : FN<4, 2, false, PREP>(__VA_ARGS__); \
     case 1:                                                                    \
-        return p.isBf16 ? FN<4, 1, true>(__VA_ARGS__) : FN<4, 1, false>(__VA_ARGS__); \
+        return p.isBf16 ? FN<4, 1, true, PREP>(__VA_ARGS__) : FN<4, 1, false, PREP>(__VA_ARGS__); \
     default:                                                                   \
         break;                                                                 \
+    }
+#define MHC_FUSED_DISPATCH(FN, ...)                                            \
+    if (p.bprep != nullptr) {                                                  \
+        MHC_FUSED_DISPATCH_P(FN, true, __VA_ARGS__)                            \
+    } else {                                                                   \
+        MHC_FUSED_DISPATCH_P(FN, false, __VA_ARGS__)                           \
     }
 
 hipError_t launch_fused(const Plan &p, void *workspace, uint32_t launchId, hipStream_t stream)

@@ -116,6 +116,9 @@ struct Plan {
     float *hPost = nullptr;
     float *hRes = nullptr;
     float *hPre = nullptr;
+    // Prepared B operand (mhcPrePrepareWeights), or null: the kernels then
+    // build B from phi and gamma.  Layout of launch_prepare_b.
+    const void *bprep = nullptr;
 };
 
 // Built-in workspace of mhcPreNoAlloc (mhc_pre_noalloc.hip): kScratchBytes
@@ -132,6 +135,17 @@ hipError_t launch_split(const Plan &plan, void *workspace, hipStream_t stream);
 hipError_t launch_fused(const Plan &plan, void *workspace, uint32_t launchId, hipStream_t stream);
 
 hipError_t launch_strip(const Plan &plan, void *workspace, uint32_t launchId, hipStream_t stream);
+
+// Prepared B operand (mhc_pre_rows.hip): B = gamma (.) phi (gamma may be
+// null) split into bf16 hi + lo MFMA fragments, [K/32 k-steps][2M/16 column
+// tiles][64 lanes] x 16 bytes.  Lane l of fragment (ks, t) holds k = 32 ks +
+// 8 (l / 16) .. + 7 of one column: tile t < Q = M/16 the hi half of column
+// 16 t + l % 16, tile Q + t the lo half of the same column; when M % 16 == 8
+// tile 2Q holds column 16 Q + l % 8, hi in lanes l % 16 < 8 and lo in the
+// others.  The strip and fused kernels keep B in LDS in this same column
+// order, and the rows path's GEMM reads it as it is.
+hipError_t launch_prepare_b(int n, const float *phi, const float *gamma, void *bfrag, int64_t K,
+                            hipStream_t stream);
 
 // Rows path (mhc_pre_rows.hip); nXcd: XCDs of the device (work placement
 // only).

@@ -77,6 +77,45 @@ __global__ __launch_bounds__(256) void prep_b_kernel(const float *__restrict__ p
 }
 
 // ---------------------------------------------------------------------------
+// split_b_from_prepared: the same fragments from prepared weights (layout of
+// launch_prepare_b: per k-step, tile t < Q = M/16 holds hi of columns
+// 16t + l%16, tile Q + t their lo, and when M % 16 == 8 tile 2Q holds hi
+// (lanes l%16 < 8) and lo (the others) of column 16Q + l%8).  Every 16-byte
+// fragment lane is copied from the prepared lane holding the same column
+// half and k.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void split_b_from_prepared_kernel(const u32x4_t *__restrict__ src,
+                                                                    u32x4_t *__restrict__ bsplit,
+                                                                    int64_t K, int M, int NT,
+                                                                    uint32_t *__restrict__ status)
+{
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx == 0 && status != nullptr) {
+        *status = kDeviceOk;
+    }
+    const int64_t total = (K / 32) * NT * kWave;
+    if (idx >= total) {
+        return;
+    }
+    const int lane = (int)(idx % kWave);
+    const int ct = (int)((idx / kWave) % NT);
+    const int64_t ks = idx / ((int64_t)kWave * NT);
+    const int c = 16 * ct + (lane & 15);
+    const bool lo = c >= M;
+    const int j = lo ? c - M : c;
+    const int Q = M / 16;
+    int tile, sl;
+    if (j < 16 * Q) {
+        tile = (lo ? Q : 0) + j / 16;
+        sl = (j % 16) + 16 * (lane >> 4);
+    } else {
+        tile = 2 * Q;
+        sl = (j - 16 * Q) + (lo ? 8 : 0) + 16 * (lane >> 4);
+    }
+    bsplit[idx] = src[(ks * NT + tile) * kWave + sl];
+}
+
+// ---------------------------------------------------------------------------
 // gemm_partial: one workgroup = 4 waves = one 16-row tile x one K-slice.
 // Waves interleave the slice's 32-wide k-steps; the workgroup reduces its
 // waves through LDS in wave order and writes
@@ -279,9 +318,15 @@ hipError_t launch_split_t(const Plan &p, void *workspace, hipStream_t stream)
     float *partial = reinterpret_cast<float *>(ws + p.wsPartial);
 
     const int64_t prepThreads = (p.K / 32) * p.NT * kWave;
-    hipLaunchKernelGGL(prep_b_kernel, dim3((unsigned)((prepThreads + 255) / 256)), dim3(256), 0,
-                       stream, p.phi, p.hasGamma ? p.gamma : nullptr, bsplit, p.K, p.M, p.NT,
-                       status);
+    if (p.bprep != nullptr) {
+        hipLaunchKernelGGL(split_b_from_prepared_kernel, dim3((unsigned)((prepThreads + 255) / 256)),
+                           dim3(256), 0, stream, static_cast<const u32x4_t *>(p.bprep), bsplit, p.K,
+                           p.M, p.NT, status);
+    } else {
+        hipLaunchKernelGGL(prep_b_kernel, dim3((unsigned)((prepThreads + 255) / 256)), dim3(256), 0,
+                           stream, p.phi, p.hasGamma ? p.gamma : nullptr, bsplit, p.K, p.M, p.NT,
+                           status);
+    }
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) {
         return err;

@@ -483,19 +483,22 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
 // rows (four 16-row blocks, rows past T read as zeros) and builds its B
 // fragments from phi and gamma in registers, so no prepared copy of B is
 // written or read: with one row block, every element of B is used once.
-// The waves' partial sums meet in LDS and are added in wave order.
+// With prepared weights (kPrep) it loads its fragments from the prepared
+// buffer instead.  The waves' partial sums meet in LDS and are added in wave
+// order.
 // ---------------------------------------------------------------------------
 struct RowsSmallArgs {
     const uint16_t *x;
     const float *phi;
     const float *gamma;
+    const u32x4_t *bprep;  // prepared B fragments [K/32][NT][64] (kPrep only)
     float *partial;    // [S][T][M + 1]
     uint32_t *status;  // low half of the device status word
     int64_t T;
     int64_t K;
 };
 
-template <int N, bool kBf16>
+template <int N, bool kBf16, bool kPrep>
 __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallArgs a)
 {
     using C = RowsCols<N>;
@@ -542,29 +545,43 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
         }
     }
     // phi rows as whole 256-byte runs (the wave's 64 k of 4 rows per load),
-    // into LDS in row order; read back below in B-fragment order.
-    constexpr int kPhiLoads = M / 4;
+    // into LDS in row order; read back below in B-fragment order.  Prepared
+    // weights: the wave's NT fragments of each k-step instead.
+    constexpr int kPhiLoads = kPrep ? 1 : M / 4;
     static_assert(M % 4 == 0, "4 phi rows per load");
     f32x4_t phl[kPhiLoads];
-#pragma unroll
-    for (int i = 0; i < kPhiLoads; ++i) {
-        const int j = 4 * i + (lane >> 4);
-        phl[i] = *reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + ks0 * 32 + 4 * (lane & 15));
-    }
     f32x4_t gm[kSmallKs][2];
+    u32x4_t pf[kSmallKs][kPrep ? C::NT : 1];
+    if constexpr (kPrep) {
 #pragma unroll
-    for (int kk = 0; kk < kSmallKs; ++kk) {
-        const int64_t k0 = (ks0 + kk) * 32 + 8 * (lane >> 4);
-        const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(a.gamma != nullptr ? a.gamma + k0 : a.phi);
-        gm[kk][0] = gsrc[0];
-        gm[kk][1] = gsrc[1];
+        for (int kk = 0; kk < kSmallKs; ++kk) {
+#pragma unroll
+            for (int t = 0; t < C::NT; ++t) {
+                pf[kk][t] = a.bprep[((ks0 + kk) * C::NT + t) * kWave + lane];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kPhiLoads; ++i) {
+            const int j = 4 * i + (lane >> 4);
+            phl[i] = *reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)j * a.K + ks0 * 32 + 4 * (lane & 15));
+        }
+#pragma unroll
+        for (int kk = 0; kk < kSmallKs; ++kk) {
+            const int64_t k0 = (ks0 + kk) * 32 + 8 * (lane >> 4);
+            const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(a.gamma != nullptr ? a.gamma + k0 : a.phi);
+            gm[kk][0] = gsrc[0];
+            gm[kk][1] = gsrc[1];
+        }
     }
     // Every load is issued before any use: one memory round trip.
     __builtin_amdgcn_sched_barrier(0);
 
+    if constexpr (!kPrep) {
 #pragma unroll
-    for (int i = 0; i < kPhiLoads; ++i) {
-        *reinterpret_cast<f32x4_t *>(stage + (4 * i + (lane >> 4)) * kPhiPitch + 4 * (lane & 15)) = phl[i];
+        for (int i = 0; i < kPhiLoads; ++i) {
+            *reinterpret_cast<f32x4_t *>(stage + (4 * i + (lane >> 4)) * kPhiPitch + 4 * (lane & 15)) = phl[i];
+        }
     }
     u32x4_t xa[kSmallKs][RB];
 #pragma unroll
@@ -575,14 +592,16 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     // the half tile's lanes 8-15 hold the lo half of the column of lanes 0-7.
     // (The wave reads only its own staging block, which it wrote above.)
     f32x4_t ph[kSmallKs][NA][2];
+    if constexpr (!kPrep) {
 #pragma unroll
-    for (int kk = 0; kk < kSmallKs; ++kk) {
+        for (int kk = 0; kk < kSmallKs; ++kk) {
 #pragma unroll
-        for (int ta = 0; ta < NA; ++ta) {
-            const int j = ta < Q ? 16 * ta + (lane & 15) : 16 * Q + (lane & 7);
-            const float *src = stage + j * kPhiPitch + 32 * kk + 8 * (lane >> 4);
-            ph[kk][ta][0] = *reinterpret_cast<const f32x4_t *>(src);
-            ph[kk][ta][1] = *reinterpret_cast<const f32x4_t *>(src + 4);
+            for (int ta = 0; ta < NA; ++ta) {
+                const int j = ta < Q ? 16 * ta + (lane & 15) : 16 * Q + (lane & 7);
+                const float *src = stage + j * kPhiPitch + 32 * kk + 8 * (lane >> 4);
+                ph[kk][ta][0] = *reinterpret_cast<const f32x4_t *>(src);
+                ph[kk][ta][1] = *reinterpret_cast<const f32x4_t *>(src + 4);
+            }
         }
     }
 
@@ -610,21 +629,28 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
         }
 #pragma unroll
         for (int ta = 0; ta < NA; ++ta) {
-            float b[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                b[e] = ph[kk][ta][e >> 2][e & 3];
-                if (hasGamma) {
-                    b[e] = b[e] * gm[kk][e >> 2][e & 3];
-                }
-            }
             u32x4_t bh, bl;
+            if constexpr (kPrep) {
+                // Tile ta holds hi of its columns, tile Q + ta their lo; the
+                // half tile (ta == Q) is hi and lo in one fragment.
+                bh = pf[kk][ta < Q ? ta : 2 * Q];
+                bl = pf[kk][ta < Q ? Q + ta : 2 * Q];
+            } else {
+                float b[8];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                uint32_t h, l;
-                split2_bf16(b[2 * w], b[2 * w + 1], h, l);
-                bh[w] = h;
-                bl[w] = l;
+                for (int e = 0; e < 8; ++e) {
+                    b[e] = ph[kk][ta][e >> 2][e & 3];
+                    if (hasGamma) {
+                        b[e] = b[e] * gm[kk][e >> 2][e & 3];
+                    }
+                }
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    uint32_t h, l;
+                    split2_bf16(b[2 * w], b[2 * w + 1], h, l);
+                    bh[w] = h;
+                    bl[w] = l;
+                }
             }
             if (ta < Q) {
 #pragma unroll
@@ -639,8 +665,9 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
                     }
                 }
             } else {
-                // Half tile: hi in lanes 0-7 of each 16, lo in lanes 8-15.
-                const u32x4_t bq = (lane & 15) < 8 ? bh : bl;
+                // Half tile: hi in lanes 0-7 of each 16, lo in lanes 8-15
+                // (a prepared fragment holds them so already).
+                const u32x4_t bq = kPrep ? bh : ((lane & 15) < 8 ? bh : bl);
 #pragma unroll
                 for (int r = 0; r < RB; ++r) {
                     if constexpr (kBf16) {
@@ -911,29 +938,38 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
     using C = RowsCols<N>;
     hipError_t err = hipSuccess;
 
+    const u32x4_t *bprep = static_cast<const u32x4_t *>(p.bprep);
     if (p.rowsSmall) {
         RowsSmallArgs sa;
         sa.x = static_cast<const uint16_t *>(p.x);
         sa.phi = p.phi;
         sa.gamma = p.hasGamma ? p.gamma : nullptr;
+        sa.bprep = bprep;
         sa.partial = partial;
         sa.status = status;
         sa.T = p.T;
         sa.K = p.K;
-        hipLaunchKernelGGL((rows_small_kernel<N, kBf16>), dim3((unsigned)p.rowsS),
-                           dim3(kSmallWaves * 64), 0, stream, sa);
+        if (bprep != nullptr) {
+            hipLaunchKernelGGL((rows_small_kernel<N, kBf16, true>), dim3((unsigned)p.rowsS),
+                               dim3(kSmallWaves * 64), 0, stream, sa);
+        } else {
+            hipLaunchKernelGGL((rows_small_kernel<N, kBf16, false>), dim3((unsigned)p.rowsS),
+                               dim3(kSmallWaves * 64), 0, stream, sa);
+        }
     } else {
-        const int64_t prepThreads = (p.K / 32) * C::NA * kWave;
-        hipLaunchKernelGGL((rows_prep_b_kernel<N>), dim3((unsigned)((prepThreads + 255) / 256)),
-                           dim3(256), 0, stream, p.phi, p.hasGamma ? p.gamma : nullptr, bfrag, p.K,
-                           status);
-        err = hipGetLastError();
-        if (err != hipSuccess) {
-            return err;
+        if (bprep == nullptr) {
+            const int64_t prepThreads = (p.K / 32) * C::NA * kWave;
+            hipLaunchKernelGGL((rows_prep_b_kernel<N>), dim3((unsigned)((prepThreads + 255) / 256)),
+                               dim3(256), 0, stream, p.phi, p.hasGamma ? p.gamma : nullptr, bfrag, p.K,
+                               status);
+            err = hipGetLastError();
+            if (err != hipSuccess) {
+                return err;
+            }
         }
         RowsGemmArgs g;
         g.x = static_cast<const uint16_t *>(p.x);
-        g.bfrag = bfrag;
+        g.bfrag = bprep != nullptr ? bprep : bfrag;
         g.partial = partial;
         g.T = p.T;
         g.K = p.K;
@@ -994,6 +1030,39 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
 }
 
 }  // namespace
+
+hipError_t launch_prepare_b(int n, const float *phi, const float *gamma, void *bfrag, int64_t K,
+                            hipStream_t stream)
+{
+    int na = 0;
+    switch (n) {
+    case 4:
+        na = RowsCols<4>::NA;
+        break;
+    case 6:
+        na = RowsCols<6>::NA;
+        break;
+    case 8:
+        na = RowsCols<8>::NA;
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    const int64_t threads = (K / 32) * na * kWave;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    u32x4_t *dst = static_cast<u32x4_t *>(bfrag);
+    if (n == 4) {
+        hipLaunchKernelGGL((rows_prep_b_kernel<4>), grid, dim3(256), 0, stream, phi, gamma, dst, K,
+                           static_cast<uint32_t *>(nullptr));
+    } else if (n == 6) {
+        hipLaunchKernelGGL((rows_prep_b_kernel<6>), grid, dim3(256), 0, stream, phi, gamma, dst, K,
+                           static_cast<uint32_t *>(nullptr));
+    } else {
+        hipLaunchKernelGGL((rows_prep_b_kernel<8>), grid, dim3(256), 0, stream, phi, gamma, dst, K,
+                           static_cast<uint32_t *>(nullptr));
+    }
+    return hipGetLastError();
+}
 
 int rows_block_rows() { return kRowBlock; }
 int rows_gemm_threads() { return kRW * 64; }

@@ -96,6 +96,7 @@ struct StripArgs {
     const uint16_t *x;
     const float *phi;
     const float *gamma;
+    const u32x4_t *bprep;  // prepared B fragments [K/32][NT][64] (kPrep only)
     const float *alpha;
     const float *bias;
     uint16_t *hIn;
@@ -476,7 +477,7 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
     }
 }
 
-template <int N, bool kBf16>
+template <int N, bool kBf16, bool kPrep>
 __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
 {
     using S = Shape<N>;
@@ -626,20 +627,44 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const bool hasGamma = a.gamma != nullptr;
     f32x4_t ph[KW][NA][2];
     f32x4_t gm[KW][2];
+    // Prepared weights (kPrep): the fragments already have this layout; k-step
+    // ks of the strip is the prepared k-step (s D + col0 + 32 q) / 32.
+    // The copy into LDS goes out before the x ring loads, so that the
+    // fragments' registers are free again while the ring fills.
+    if constexpr (kPrep) {
+        u32x4_t pf[KW][NT];
 #pragma unroll
-    for (int i = 0; i < KW; ++i) {
-        const int ks = half + kGroups * i;
-        const int64_t k0 = (int64_t)(ks >> 1) * a.D + col0 + 32 * (ks & 1) + 8 * grp;
+        for (int i = 0; i < KW; ++i) {
+            const int ks = half + kGroups * i;
+            const int64_t gks = ((int64_t)(ks >> 1) * a.D + col0 + 32 * (ks & 1)) / 32;
 #pragma unroll
-        for (int ta = 0; ta < NA; ++ta) {
-            const int jc = ta < Q ? 16 * ta + rl : 16 * Q + (rl & 7);
-            const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)jc * a.K + k0);
-            ph[i][ta][0] = src[0];
-            ph[i][ta][1] = src[1];
+            for (int t = 0; t < NT; ++t) {
+                pf[i][t] = a.bprep[(gks * NT + t) * 64 + lane];
+            }
         }
-        const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(hasGamma ? a.gamma + k0 : a.phi);
-        gm[i][0] = gsrc[0];
-        gm[i][1] = gsrc[1];
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                bfr[half + kGroups * i][t][lane] = pf[i][t];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+            const int ks = half + kGroups * i;
+            const int64_t k0 = (int64_t)(ks >> 1) * a.D + col0 + 32 * (ks & 1) + 8 * grp;
+#pragma unroll
+            for (int ta = 0; ta < NA; ++ta) {
+                const int jc = ta < Q ? 16 * ta + rl : 16 * Q + (rl & 7);
+                const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)jc * a.K + k0);
+                ph[i][ta][0] = src[0];
+                ph[i][ta][1] = src[1];
+            }
+            const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(hasGamma ? a.gamma + k0 : a.phi);
+            gm[i][0] = gsrc[0];
+            gm[i][1] = gsrc[1];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     // The ring: slot jj mod L holds own tile jj.  Tiles 0 .. L-E-1 are loaded
@@ -659,32 +684,34 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!kPrep) {  // (prepared fragments were copied above)
 #pragma unroll
-    for (int i = 0; i < KW; ++i) {
-        const int ks = half + kGroups * i;
+        for (int i = 0; i < KW; ++i) {
+            const int ks = half + kGroups * i;
 #pragma unroll
-        for (int ta = 0; ta < NA; ++ta) {
-            float bv[8];
+            for (int ta = 0; ta < NA; ++ta) {
+                float bv[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                bv[e] = ph[i][ta][e >> 2][e & 3];
-                if (hasGamma) {
-                    bv[e] = bv[e] * gm[i][e >> 2][e & 3];
+                for (int e = 0; e < 8; ++e) {
+                    bv[e] = ph[i][ta][e >> 2][e & 3];
+                    if (hasGamma) {
+                        bv[e] = bv[e] * gm[i][e >> 2][e & 3];
+                    }
                 }
-            }
-            u32x4_t hv, lv;  // bf16(B) and bf16(B - hi)
+                u32x4_t hv, lv;  // bf16(B) and bf16(B - hi)
 #pragma unroll
-            for (int w2 = 0; w2 < 4; ++w2) {
-                uint32_t h, l;
-                split2_bf16(bv[2 * w2], bv[2 * w2 + 1], h, l);
-                hv[w2] = h;
-                lv[w2] = l;
-            }
-            if (ta < Q) {
-                bfr[ks][ta][lane] = hv;
-                bfr[ks][Q + ta][lane] = lv;
-            } else {
-                bfr[ks][2 * Q][lane] = rl < 8 ? hv : lv;  // half tile: hi in lanes 0-7
+                for (int w2 = 0; w2 < 4; ++w2) {
+                    uint32_t h, l;
+                    split2_bf16(bv[2 * w2], bv[2 * w2 + 1], h, l);
+                    hv[w2] = h;
+                    lv[w2] = l;
+                }
+                if (ta < Q) {
+                    bfr[ks][ta][lane] = hv;
+                    bfr[ks][Q + ta][lane] = lv;
+                } else {
+                    bfr[ks][2 * Q][lane] = rl < 8 ? hv : lv;  // half tile: hi in lanes 0-7
+                }
             }
         }
     }
@@ -987,19 +1014,19 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     }
 }
 
-template <int N, bool kBf16>
+template <int N, bool kBf16, bool kPrep>
 int strip_coresident_t(int numCUs)
 {
     int perCU = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &perCU, reinterpret_cast<const void *>(&strip_kernel<N, kBf16>), kWaves * 64, 0) !=
+            &perCU, reinterpret_cast<const void *>(&strip_kernel<N, kBf16, kPrep>), kWaves * 64, 0) !=
         hipSuccess) {
         return -1;
     }
     return perCU * numCUs;
 }
 
-template <int N, bool kBf16>
+template <int N, bool kBf16, bool kPrep>
 hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t launchId, hipStream_t stream)
 {
     char *ws = static_cast<char *>(workspace);
@@ -1007,6 +1034,7 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t launchId, hip
     a.x = static_cast<const uint16_t *>(p.x);
     a.phi = p.phi;
     a.gamma = p.hasGamma ? p.gamma : nullptr;
+    a.bprep = static_cast<const u32x4_t *>(p.bprep);
     a.alpha = p.alpha;
     a.bias = p.bias;
     a.hIn = static_cast<uint16_t *>(p.hIn);
@@ -1032,14 +1060,14 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t launchId, hip
     a.launchId = launchId;
     a.spinLimit = p.spinLimit;
     if (!p.fusedCooperative) {
-        hipLaunchKernelGGL((strip_kernel<N, kBf16>), dim3((unsigned)p.stripGrid), dim3(kWaves * 64), 0,
+        hipLaunchKernelGGL((strip_kernel<N, kBf16, kPrep>), dim3((unsigned)p.stripGrid), dim3(kWaves * 64), 0,
                            stream, a);
         return hipGetLastError();
     }
     // Cooperative launch (MHCPRE_LAUNCH=cooperative): co-residency of the
     // whole grid is guaranteed even next to concurrent work.
     void *args[] = {&a};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&strip_kernel<N, kBf16>),
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&strip_kernel<N, kBf16, kPrep>),
                                       dim3((unsigned)p.stripGrid), dim3(kWaves * 64), args, 0,
                                       stream);
 }
@@ -1051,8 +1079,12 @@ hipError_t launch_strip(const Plan &p, void *workspace, uint32_t launchId, hipSt
     if (p.n != 4) {
         return hipErrorNotSupported;
     }
-    return p.isBf16 ? launch_strip_t<4, true>(p, workspace, launchId, stream)
-                    : launch_strip_t<4, false>(p, workspace, launchId, stream);
+    if (p.bprep != nullptr) {
+        return p.isBf16 ? launch_strip_t<4, true, true>(p, workspace, launchId, stream)
+                        : launch_strip_t<4, false, true>(p, workspace, launchId, stream);
+    }
+    return p.isBf16 ? launch_strip_t<4, true, false>(p, workspace, launchId, stream)
+                    : launch_strip_t<4, false, false>(p, workspace, launchId, stream);
 }
 
 int strip_ring_slots() { return kRingSlots; }
@@ -1069,7 +1101,12 @@ int strip_max_coresident(const Plan &p, int numCUs)
     if (p.n != 4) {
         return -1;
     }
-    return p.isBf16 ? strip_coresident_t<4, true>(numCUs) : strip_coresident_t<4, false>(numCUs);
+    if (p.bprep != nullptr) {
+        return p.isBf16 ? strip_coresident_t<4, true, true>(numCUs)
+                        : strip_coresident_t<4, false, true>(numCUs);
+    }
+    return p.isBf16 ? strip_coresident_t<4, true, false>(numCUs)
+                    : strip_coresident_t<4, false, false>(numCUs);
 }
 
 }  // namespace mhc
