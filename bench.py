@@ -148,13 +148,14 @@ def cpu_baseline(x, phi, alpha, bias, gamma, bf16: bool, target_s: float) -> dic
             "cpu_model": cpu_model()}
 
 
-def measured_traffic(workload: str, path: str):
+def measured_traffic(workload: str, path: str, prepared: bool = False):
     """HBM bytes per launch for this workload from the committed rocprofv3 PMC
     record (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size) of the
-    kernel path this launch takes, or None."""
+    kernel path this launch takes (and the same weights mode), or None."""
     for f in sorted((ROOT / "profiles").glob("*.traffic.json")):
         rec = json.loads(f.read_text())
-        if rec.get("workload") == workload and rec.get("path") == path:
+        if (rec.get("workload") == workload and rec.get("path") == path
+                and bool(rec.get("prepared_weights", False)) == prepared):
             return rec
     return None
 
@@ -172,6 +173,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=3, choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target duration of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--prepared", action="store_true",
+                    help="launch an executor built from prepared weights (mhcPrePrepareWeights)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a device copy of a known size (calibrates profiler byte counters)")
     args = ap.parse_args()
@@ -192,7 +195,14 @@ def main() -> int:
     device = torch.device("cuda:0")
     n, D, T, bf16, gamma_on, _ = WORKLOADS[args.config]
     x, phi, alpha, bias, gamma = make_inputs(args.config, device)
-    op = pkg.MhcPreOp(x, phi, alpha, bias, gamma)
+    weights = None
+    if args.prepared:
+        # B = gamma * phi prepared once, outside the timed region (the
+        # weights of a layer do not change between steps).
+        weights = pkg.MhcPreWeights(phi, gamma, n)
+        op = pkg.MhcPreOp(x, None, alpha, bias, None, weights=weights)
+    else:
+        op = pkg.MhcPreOp(x, phi, alpha, bias, gamma)
     stream = torch.cuda.current_stream()
 
     # Clock settling: launches back to back for settle_ms of wall time (the
@@ -315,7 +325,7 @@ def main() -> int:
     achieved = b_alg / (roof_us * 1e-6) / 1e9
     workload = (f"mhc_pre n={n} D={D} T={T} {'bf16' if bf16 else 'fp16'} "
                 f"gamma={'on' if gamma_on else 'off'}")
-    traffic = measured_traffic(workload, op.path)
+    traffic = measured_traffic(workload, op.path, args.prepared)
     result = {
         "metric": METRIC,
         "value": T / (mean_ms * 1e-3),
@@ -333,6 +343,7 @@ def main() -> int:
         "settle_launches": settle_launches,
         "config": {"workload": workload,
                    "n": n, "D": D, "T": T, "gamma": gamma_on, "path": op.path,
+                   "prepared_weights": args.prepared,
                    "launch_us": mean_ms * 1e3,
                    "event_pair_median_us": durs[len(durs) // 2] * 1e3,
                    "event_pair_min_us": durs[0] * 1e3,
