@@ -232,6 +232,27 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Workgroup-wide AND of ok through LDS, with a barrier that orders LDS only
+// (__syncthreads_and also waits for the workgroup's outstanding global
+// stores).  The two halves of votes are used alternately: a wave writes one
+// half again only after the barrier of the other half, which every wave
+// reaches after reading this one.
+__device__ __forceinline__ bool wg_all(bool ok, uint32_t *votes, uint32_t &parity)
+{
+    const int w = (int)(threadIdx.x >> 6);
+    const bool waveOk = __all(ok) != 0;
+    uint32_t *half = votes + parity * kWaves;
+    parity ^= 1u;
+    if ((threadIdx.x & 63) == 0) {
+        half[w] = waveOk ? 1u : 0u;
+    }
+    const u32x4_t *v = reinterpret_cast<const u32x4_t *>(half);
+    lds_barrier();
+    const u32x4_t v0 = v[0];
+    const u32x4_t v1 = v[1];
+    return (v0[0] & v0[1] & v0[2] & v0[3] & v1[0] & v1[1] & v1[2] & v1[3]) != 0u;
+}
+
 // A fragments of k-steps 2q and 2q + 1 from the line-layout registers r0
 // (rows 0-7) and r1 (rows 8-15): lanes with bit 3 set take the other
 // register's lane l ^ 8 (DPP row_ror:8 with banks 2-3 or 0-1 enabled).
@@ -327,6 +348,11 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
                                                                               : Poll2::SG * Poll2::ITEMS;
     float *sums = lds;                // [SG][ITEMS][2] of the current phase
     float *irs = lds + 2 * kSums;     // [16] invRms per row
+    uint32_t *votes = reinterpret_cast<uint32_t *>(lds + 2 * kSums + 16);  // [2][kWaves]
+    static_assert((2 * kSums + 16) % 4 == 0, "vote words 16-byte aligned");
+    static_assert(kWaves == 8, "wg_all reads two 16-byte vote vectors");
+    static_assert(8 * (N + 1) <= 64, "phase 1 is finished by one wave");
+    uint32_t voteParity = 0;
     const int tid = threadIdx.x;
     const int P = a.P;
     // The launch's exchange epoch: read by thread 0 from the workspace header
@@ -360,7 +386,7 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
         for (uint32_t spins = 0;; ++spins) {
             p1.issue(tr, P);
             const bool ok = p1.sum(tileBase, epoch, P, acc);
-            if (__syncthreads_and(ok) != 0) {
+            if (wg_all(ok, votes, voteParity)) {
                 got = true;
                 break;
             }
@@ -382,27 +408,41 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
             sums[(p1.sg * Poll1::ITEMS + tid % Poll1::ITEMS) * 2 + 1] = acc.y;
         }
         lds_barrier();
-        float2 tot = make_float2(0.f, 0.f);
-        if (tid < Poll1::ITEMS) {
+        // Wave 0 finishes phase 1 (its lanes 0 .. 8(N+1)-1 are the items):
+        // the groups' sums in order, invRms in the lanes of column N (lane
+        // 8N + i has rows 2i, 2i + 1), handed to the hPre lanes of the same
+        // rows by a shuffle and to phase 2 through LDS (read after the next
+        // barrier).
+        if (tid < 64) {
+            float2 gs[Poll1::SG];
 #pragma unroll
             for (int g = 0; g < Poll1::SG; ++g) {
-                tot.x = tot.x + sums[(g * Poll1::ITEMS + tid) * 2];
-                tot.y = tot.y + sums[(g * Poll1::ITEMS + tid) * 2 + 1];
+                gs[g] = tid < Poll1::ITEMS ? *reinterpret_cast<const float2 *>(&sums[(g * Poll1::ITEMS + tid) * 2])
+                                           : make_float2(0.f, 0.f);
             }
-            if (p1.c == N) {  // sum of squares: invRms of rows r0, r0 + 1
-                irs[p1.r0] = ref_inv_rms(tot.x, a.invFlatDim, a.normEps);
-                irs[p1.r0 + 1] = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
+            float2 tot = make_float2(0.f, 0.f);
+#pragma unroll
+            for (int g = 0; g < Poll1::SG; ++g) {
+                tot.x = tot.x + gs[g].x;
+                tot.y = tot.y + gs[g].y;
             }
-        }
-        lds_barrier();
-        if (tid < Poll1::ITEMS && p1.c < N) {
+            float ir2[2] = {0.f, 0.f};
+            if (tid < Poll1::ITEMS && p1.c == N) {  // sum of squares: invRms of rows r0, r0 + 1
+                ir2[0] = ref_inv_rms(tot.x, a.invFlatDim, a.normEps);
+                ir2[1] = ref_inv_rms(tot.y, a.invFlatDim, a.normEps);
+                irs[p1.r0] = ir2[0];
+                irs[p1.r0 + 1] = ir2[1];
+            }
+            ir2[0] = __shfl(ir2[0], 8 * N + (tid & 7));
+            ir2[1] = __shfl(ir2[1], 8 * N + (tid & 7));
+            if (tid < Poll1::ITEMS && p1.c < N) {
             // hPre column c: broadcast words (rows r0, r0 + 1) and the
             // optional hPre output.
             const int c = p1.c;
             u32x4_t wv;
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const float ir = irs[p1.r0 + e];
+                const float ir = ir2[e];
                 const float mix = e == 0 ? tot.x : tot.y;
                 const float v = ref_sigmoid(mix * (ir * alphaPre), bias1, a.hcEps);
                 const int idx = c * 16 + p1.r0 + e;
@@ -419,6 +459,7 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
             } else {
                 store16<kCpolDev>(wv, br, (c * 16 + p1.r0) * 8);
             }
+            }
         }
 
         // Phase 2: hPost / hRes columns.
@@ -426,7 +467,7 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
         for (uint32_t spins = 0;; ++spins) {
             p2.issue(tr, P);
             const bool ok = p2.sum(tileBase, epoch, P, acc);
-            if (__syncthreads_and(ok) != 0) {
+            if (wg_all(ok, votes, voteParity)) {
                 got = true;
                 break;
             }
@@ -449,11 +490,16 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
         }
         lds_barrier();
         if (tid < Poll2::ITEMS) {
-            tot = make_float2(0.f, 0.f);
+            float2 gs[Poll2::SG];
 #pragma unroll
             for (int g = 0; g < Poll2::SG; ++g) {
-                tot.x = tot.x + sums[(g * Poll2::ITEMS + tid) * 2];
-                tot.y = tot.y + sums[(g * Poll2::ITEMS + tid) * 2 + 1];
+                gs[g] = *reinterpret_cast<const float2 *>(&sums[(g * Poll2::ITEMS + tid) * 2]);
+            }
+            float2 tot = make_float2(0.f, 0.f);
+#pragma unroll
+            for (int g = 0; g < Poll2::SG; ++g) {
+                tot.x = tot.x + gs[g].x;
+                tot.y = tot.y + gs[g].y;
             }
             // Mix column j = c - 1 (N .. M-1): hPost or hRes.
             const int jj = p2.c - 1;
@@ -722,14 +768,15 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     lds_barrier();
     const uint32_t epoch = __builtin_amdgcn_readfirstlane(epochSh);
 
-    // Every step issues the same memory operations in the same order (two
-    // hIn stores, one broadcast poll, eight x loads, one record store per
-    // lane), whatever the step: out-of-range tiles go through size-0
-    // resources and polls of out-of-range tiles re-read the team's first
-    // block and are ignored.  With no data-dependent branch around a memory
-    // operation, the compiler's wait counts stay exact and no wait drains the
-    // ring.  The poll of step jj serves the hIn of step jj + 1; the x loads
-    // and the record store of step jj are behind it.
+    // Every step of the main loop issues the same memory operations in the
+    // same order (two hIn stores, one broadcast poll, eight x loads, one
+    // record store per lane), whatever the step: out-of-range tiles go
+    // through size-0 resources and polls of out-of-range tiles re-read the
+    // team's first block and are ignored.  With no data-dependent branch
+    // around a memory operation, the compiler's wait counts stay exact and no
+    // wait drains the ring.  The poll of step jj serves the hIn of step
+    // jj + 1; the x loads and the record store of step jj are behind it.
+    // The drain steps, past the last tile, only write hIn.
     uint64_t pr[L];  // broadcast polls: slot j mod L for own tile j's hIn
 #pragma unroll
     for (int b = 0; b < L; ++b) {
@@ -741,14 +788,19 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     auto slot_of = [&](int jj) { return teamI * kRingSlots + (kGroups * jj + half) % kRingSlots; };
     bool timedOut = false;
 
-    // Meeting count of the other group once it has run all its steps.
+    // Meeting count of the other group once it has run all its steps (the
+    // meetings are in the steps with a tile, own steps 0 .. nmine - 1).
     const int nmineOther = (nt32 - (half ^ 1) + kGroups - 1) / kGroups;
-    const uint32_t otherCount = 4u * (uint32_t)(nmineOther + E);
+    const uint32_t otherCount = 4u * (uint32_t)nmineOther;
 
-    // One step of the pipeline: own step j0 + b, ring slot b (a compile-time
-    // constant in every copy of the body).
-    auto step = [&](int j0, auto bc) __attribute__((always_inline)) {
+    // One step of the pipeline: own step j0 + b, ring slot b mod L (a
+    // compile-time constant in every copy of the body).  A drain step (kFull
+    // false: own steps nmine .. nmine + E - 1, which have no tile of their
+    // own) runs part 1 only, the hIn of own tile jj - E.
+    auto step = [&](int j0, auto bc, auto fullc) __attribute__((always_inline)) {
         constexpr int b = decltype(bc)::value;
+        constexpr bool kFull = decltype(fullc)::value;
+        static_assert(!kFull || b < L, "a step with a tile uses ring slot b");
         // The step index is recomputed from an opaque copy, so that the
         // per-step addresses are derived in each step rather than
         // precomputed for all L unrolled steps and held in registers.
@@ -757,6 +809,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         const int rt = tile_of(jj);
         const int jh = jj - E;
         const int hb = (b - E + 2 * L) % L;  // ring slot of own tile jh (static after unrolling)
+        static_assert(b - E + 2 * L >= 0, "ring slot");
         const bool liveH = jh >= 0 && jh < nmine;
         const int rth = tile_of(jh);
 
@@ -832,6 +885,9 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (!kFull) {
+            return;
+        }
 
         // 2. GEMM of own tile jj (zeros past the last tile) and its Gram
         //    matrix, one stream at a time; after each stream's MFMAs the
@@ -990,20 +1046,25 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    // Whole rounds of L steps; then the last, partial round, whose steps past
-    // the drain are skipped (a separate copy of the body, so that the branch
-    // does not reach the main loop).
+    // Whole rounds of L steps with a tile; then a separate copy of the body
+    // (so that its branches do not reach the main loop) for the last, partial
+    // round of steps with a tile (fewer than L) and the E drain steps.
+    using Full = std::integral_constant<bool, true>;
+    using Drain = std::integral_constant<bool, false>;
     int j0 = 0;
-    for (; j0 + L <= nmine + E; j0 += L) {
-        static_for<L>([&](auto bc) __attribute__((always_inline)) { step(j0, bc); });
+    for (; j0 + L <= nmine; j0 += L) {
+        static_for<L>([&](auto bc) __attribute__((always_inline)) { step(j0, bc, Full{}); });
     }
-    if (j0 < nmine + E) {
-        static_for<L>([&](auto bc) __attribute__((always_inline)) {
-            if (j0 + decltype(bc)::value < nmine + E) {
-                step(j0, bc);
+    static_for<L + E - 1>([&](auto bc) __attribute__((always_inline)) {
+        constexpr int b = decltype(bc)::value;
+        if (j0 + b < nmine) {
+            if constexpr (b < L) {
+                step(j0, bc, Full{});
             }
-        });
-    }
+        } else if (j0 + b < nmine + E) {
+            step(j0, bc, Drain{});
+        }
+    });
     // Workgroup 0 (always a slice workgroup of team 0) advances the
     // workspace's epoch once every workgroup has taken this one.
     if (g == 0 && w == 0) {
