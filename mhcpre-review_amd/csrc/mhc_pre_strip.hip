@@ -666,13 +666,17 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     //    are loaded behind them.
     u32x4_t (*bfr)[NT][64] = bsh[strip];
     constexpr int KW = KS / kGroups;  // k-steps built per wave
-    // Mix columns per lane: hi tile t and lo tile Q + t hold the same column
-    // 16t + (l & 15), so each column is loaded once (NA tiles of columns,
-    // the half tile's lanes 8-15 repeating lanes 0-7).
-    constexpr int NA = Q + (CL::kHalfTile ? 1 : 0);
+    // Without prepared weights, wave w loads mix columns CPW w .. CPW w +
+    // CPW - 1 of phi: for each stream one 1 KB run of a column (the slice's
+    // 256 values of K, lane l holding 4 consecutive ones), and gamma of the
+    // same runs.  Whole runs read about twice as fast as the 16 columns x
+    // 64 bytes a fragment-ordered load would touch.  The runs are turned
+    // into fragments through LDS below.
+    constexpr int CPW = M / kWaves;
+    static_assert(M % kWaves == 0, "mix columns per wave");
     const bool hasGamma = a.gamma != nullptr;
-    f32x4_t ph[KW][NA][2];
-    f32x4_t gm[KW][2];
+    f32x4_t pv[N][CPW];
+    f32x4_t gv[N];
     // Prepared weights (kPrep): the fragments already have this layout; k-step
     // ks of the strip is the prepared k-step (s D + col0 + 32 q) / 32.
     // The copy into LDS goes out before the x ring loads, so that the
@@ -696,20 +700,18 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             }
         }
     } else {
+        const __amdgpu_buffer_rsrc_t phiR = make_rsrc(a.phi, M * Ki * 4);
+        const __amdgpu_buffer_rsrc_t gamR = make_rsrc(a.gamma, hasGamma ? Ki * 4 : 0);
 #pragma unroll
-        for (int i = 0; i < KW; ++i) {
-            const int ks = half + kGroups * i;
-            const int64_t k0 = (int64_t)(ks >> 1) * a.D + col0 + 32 * (ks & 1) + 8 * grp;
+        for (int s = 0; s < N; ++s) {
 #pragma unroll
-            for (int ta = 0; ta < NA; ++ta) {
-                const int jc = ta < Q ? 16 * ta + rl : 16 * Q + (rl & 7);
-                const f32x4_t *src = reinterpret_cast<const f32x4_t *>(a.phi + (int64_t)jc * a.K + k0);
-                ph[i][ta][0] = src[0];
-                ph[i][ta][1] = src[1];
+            for (int c = 0; c < CPW; ++c) {
+                pv[s][c] = __builtin_bit_cast(
+                    f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                 phiR, ((CPW * w + c) * Ki + s * Di + p * kSlice) * 4 + 16 * lane, 0, 0));
             }
-            const f32x4_t *gsrc = reinterpret_cast<const f32x4_t *>(hasGamma ? a.gamma + k0 : a.phi);
-            gm[i][0] = gsrc[0];
-            gm[i][1] = gsrc[1];
+            gv[s] = __builtin_bit_cast(
+                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gamR, (s * Di + p * kSlice) * 4 + 16 * lane, 0, 0));
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -731,33 +733,52 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (!kPrep) {  // (prepared fragments were copied above)
+        // One round per stream s, through a staging area in the partials
+        // buffer (idle until the first step): each wave writes its columns'
+        // products gamma * phi as bf16 hi and lo rows (row j: the slice's 256
+        // values of K, padded to kStagePitch bytes so that the 8 lanes of a
+        // read phase hit distinct banks), then builds 3 of the stream's 24
+        // fragments (4 strips x 2 k-steps x NT tiles) from them.
+        constexpr int kStagePitch = kSlice * 2 + 16;
+        static_assert(2 * M * kStagePitch <= (int)sizeof(part), "staging fits the partials buffer");
+        static_assert(kStrips * 2 * NT == 3 * kWaves, "fragments per wave and round");
+        char *stHi = reinterpret_cast<char *>(&part[0][0][0][0]);
+        char *stLo = stHi + M * kStagePitch;
 #pragma unroll
-        for (int i = 0; i < KW; ++i) {
-            const int ks = half + kGroups * i;
+        for (int s = 0; s < N; ++s) {
 #pragma unroll
-            for (int ta = 0; ta < NA; ++ta) {
-                float bv[8];
+            for (int c = 0; c < CPW; ++c) {
+                float bv[4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    bv[e] = ph[i][ta][e >> 2][e & 3];
+                for (int e = 0; e < 4; ++e) {
+                    bv[e] = pv[s][c][e];
                     if (hasGamma) {
-                        bv[e] = bv[e] * gm[i][e >> 2][e & 3];
+                        bv[e] = bv[e] * gv[s][e];
                     }
                 }
-                u32x4_t hv, lv;  // bf16(B) and bf16(B - hi)
+                uint32_t h0, l0, h1, l1;  // bf16(B) and bf16(B - hi), k pairs (4l, 4l+1), (4l+2, 4l+3)
+                split2_bf16(bv[0], bv[1], h0, l0);
+                split2_bf16(bv[2], bv[3], h1, l1);
+                const int off = (CPW * w + c) * kStagePitch + 8 * lane;
+                *reinterpret_cast<uint2 *>(stHi + off) = make_uint2(h0, h1);
+                *reinterpret_cast<uint2 *>(stLo + off) = make_uint2(l0, l1);
+            }
+            lds_barrier();
 #pragma unroll
-                for (int w2 = 0; w2 < 4; ++w2) {
-                    uint32_t h, l;
-                    split2_bf16(bv[2 * w2], bv[2 * w2 + 1], h, l);
-                    hv[w2] = h;
-                    lv[w2] = l;
-                }
-                if (ta < Q) {
-                    bfr[ks][ta][lane] = hv;
-                    bfr[ks][Q + ta][lane] = lv;
-                } else {
-                    bfr[ks][2 * Q][lane] = rl < 8 ? hv : lv;  // half tile: hi in lanes 0-7
-                }
+            for (int f0 = 0; f0 < 3; ++f0) {
+                const int f = 3 * w + f0;  // (strip, q, t) = (f / (2 NT), (f / NT) % 2, f % NT)
+                const int fs = f / (2 * NT);
+                const int fq = (f / NT) % 2;
+                const int ft = f % NT;
+                bool lo;
+                int jc;
+                CL::slot(16 * ft + rl, lo, jc);
+                const int k = 64 * fs + 32 * fq + 8 * grp;
+                bsh[fs][2 * s + fq][ft][lane] =
+                    *reinterpret_cast<const u32x4_t *>((lo ? stLo : stHi) + jc * kStagePitch + 2 * k);
+            }
+            if (s + 1 < N) {
+                lds_barrier();  // the staging rows are rewritten by the next round
             }
         }
     }
