@@ -163,6 +163,12 @@ struct Rec {
     __device__ static int col(int j) { return j < N ? j : j + 1; }
 };
 
+// Word positions are uint32 and wrap modulo 2^32 for very large T.  That is
+// harmless: a reader only ever finds, at a ring address, words of the same
+// launch's earlier occupants of that slot, k * S * numTeams * (P * WORDS or
+// BWORDS) positions apart (numTeams * P <= 256 CUs, so not a multiple of
+// 2^32 for any k below 2^17, more slot reuses than T < 2^24 rows allow), or
+// words of other launches (other epochs).
 __device__ __forceinline__ uint32_t rec_tag(uint32_t pos, uint32_t epoch)
 {
     return (pos * 0x9E3779B1u) ^ epoch;
