@@ -73,7 +73,9 @@ __global__ __launch_bounds__(256) void prep_b_kernel(const float *__restrict__ p
         const float hi = bf16_bits_to_f32(f32_to_bf16_bits(b[e]));
         out[e] = isLo ? (b[e] - hi) : hi;
     }
-    bsplit[idx] = pack8_bf16(out);
+    // Nontemporal: read by the next kernel (lines left in this XCD's L2 slow
+    // its reads of B down).
+    __builtin_nontemporal_store(pack8_bf16(out), &bsplit[idx]);
 }
 
 // ---------------------------------------------------------------------------
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(256) void split_b_from_prepared_kernel(const u32x4_
         tile = 2 * Q;
         sl = (j - 16 * Q) + (lo ? 8 : 0) + 16 * (lane >> 4);
     }
-    bsplit[idx] = src[(ks * NT + tile) * kWave + sl];
+    __builtin_nontemporal_store(src[(ks * NT + tile) * kWave + sl], &bsplit[idx]);
 }
 
 // ---------------------------------------------------------------------------
