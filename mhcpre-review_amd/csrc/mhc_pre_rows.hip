@@ -87,7 +87,8 @@ struct RowsCols {
     static constexpr bool hi_tile(int t) { return t < Q || t == 2 * Q; }
 };
 
-constexpr int kCpolNt = 2;  // nontemporal: x is streamed, hIn written once
+constexpr int kCpolNt = 2;   // nontemporal: x is streamed
+constexpr int kCpolDev = 16; // sc1: device scope, written through
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int bytes)
 {
@@ -922,10 +923,12 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
             for (int w = 0; w < 4; ++w) {
                 out[w] = pack2_x<kBf16>(acc[2 * w], acc[2 * w + 1]);
             }
+            // hIn goes out with device-scope (write-through) stores: about
+            // 3 us faster than nontemporal ones at n = 8, D = 8192, T = 5472.
             if (d8 < oEnd) {
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, out), hr,
-                    d8 * 16, 0, kCpolNt);
+                    d8 * 16, 0, kCpolDev);
             }
         }
     }
