@@ -214,9 +214,9 @@ __global__ __launch_bounds__(256) void rows_prep_b_kernel(const float *__restric
         hi[w] = h;
         lo[w] = l;
     }
-    // Nontemporal stores: B is read by the next kernel from memory; lines
-    // left in this XCD's L2 made the block GEMM about 20 us slower at
-    // n = 8, D = 8192, T = 5472.
+    // Nontemporal stores: with plain ones the block GEMM that reads B next
+    // ran about 20 us slower at n = 8, D = 8192, T = 5472, for the same
+    // bytes fetched from memory.
     u32x4_t *dst = bfrag + ks * C::NT * kWave;
     __builtin_nontemporal_store(hi, &dst[thi * kWave + lhi]);
     __builtin_nontemporal_store(lo, &dst[tlo * kWave + llo]);
