@@ -1,0 +1,147 @@
+"""GPU parity on seeded random shapes: every launch path the plan can take.
+
+Each case draws n in {4, 6, 8}, a width D (a multiple of 16, up to 7936), a
+row count T (ragged, 1 to a few thousand), the x dtype, gamma on or off and
+random attributes (alpha up to 0.5 in magnitude, eps), runs the path the plan
+picks and one other path forced through MHCPRE_FORCE_PATH (the plan keeps its
+own choice when the forced one does not take the shape), and checks both
+against the CPU oracle at the tolerances of tests/helpers.py.  Sizes are
+bounded so that the oracle finishes each case in well under a second.
+
+The oracle sums the mixing GEMM k-sequentially in fp32 (the reference's
+vendor GEMM order is not known); with |alpha| near 0.5 and K in the tens of
+thousands its own rounding can reach the fp32 tolerance.  Where the oracle is
+further than half the tolerance from an fp64 evaluation of the same formula,
+the device value is held to the tolerance around the fp64 value instead, and
+the case reports how many elements that was.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import ATOL, RTOL, assert_hin
+from inputs import to_bits
+from test_gpu_parity import _say, run_gpu
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 64
+N_CASES_N4 = 24
+MAX_ELEMS = 6_000_000  # T * n * D per case
+
+
+def random_case(i: int):
+    rng = np.random.default_rng(0x5EED0000 + i)
+    n = int(rng.choice([4, 6, 8]))
+    # Widths that reach every path: multiples of 256 (strip), of 64 (fused),
+    # of 128 / n (rows), and of 16 only (split).
+    kind = int(rng.integers(0, 4))
+    if kind == 0:
+        D = 256 * int(rng.integers(1, 32))
+    elif kind == 1:
+        D = 64 * int(rng.integers(1, 64))
+    elif kind == 2:
+        D = 128 * int(rng.integers(1, 40))
+    else:
+        D = 16 * int(rng.integers(1, 200))
+    K = n * D
+    t_max = max(1, min(MAX_ELEMS // K, 4000))
+    T = int(np.exp(rng.uniform(0.0, np.log(t_max + 1))))  # log-uniform in 1 .. t_max
+    T = max(1, min(T, t_max))
+    is_bf16 = bool(rng.integers(0, 2))
+    has_gamma = bool(rng.integers(0, 2))
+    force = str(rng.choice(["split", "fused", "rows", "strip"]))
+    alpha = rng.uniform(-0.5, 0.5, 3).astype(np.float32)
+    norm_eps = float(rng.choice([1e-6, 1e-5]))
+    hc_eps = float(rng.choice([1e-6, 0.0]))
+    return dict(seed=i, n=n, D=D, T=T, is_bf16=is_bf16, has_gamma=has_gamma, force=force,
+                alpha=alpha, norm_eps=norm_eps, hc_eps=hc_eps, rng=rng)
+
+
+def exact_outputs(orc, x_bits, is_bf16, phi, alpha, bias, gamma, norm_eps, hc_eps):
+    """hPre, hPost, hRes of the formula evaluated in fp64 (inputs as given)."""
+    T, n, D = x_bits.shape
+    K, M = n * D, n * n + 2 * n
+    x = orc.bits_to_f32(x_bits.reshape(T, K), is_bf16).astype(np.float64)
+    w = phi.reshape(M, K).astype(np.float64)
+    if gamma is not None:
+        w = w * gamma.astype(np.float64)[None, :]
+    mix = x @ w.T
+    inv_rms = 1.0 / np.sqrt((x * x).sum(axis=1) * (1.0 / K) + norm_eps)
+    a = alpha.astype(np.float64)
+    b = bias.astype(np.float64)
+    pre = 1.0 / (1.0 + np.exp(-(mix[:, :n] * inv_rms[:, None] * a[0] + b[:n]))) + hc_eps
+    post = 2.0 / (1.0 + np.exp(-(mix[:, n:2 * n] * inv_rms[:, None] * a[1] + b[n:2 * n])))
+    res = mix[:, 2 * n:] * inv_rms[:, None] * a[2] + b[2 * n:]
+    return {"h_pre": pre, "h_post": post, "h_res": res.reshape(T, n, n)}
+
+
+def close_to_oracle_or_exact(name, got, want, exact):
+    """Every element within tolerance of the oracle, or, where the oracle is
+    more than half the tolerance off the fp64 value, of the fp64 value.
+    Returns how many elements took the second branch."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert np.isfinite(got).all(), f"{name}: non-finite values"
+    tol = ATOL + RTOL * np.abs(exact)
+    ok_oracle = np.abs(got - want) <= ATOL + RTOL * np.abs(want)
+    oracle_off = np.abs(want - exact) > 0.5 * tol
+    ok_exact = oracle_off & (np.abs(got - exact) <= tol)
+    bad = ~(ok_oracle | ok_exact)
+    if bad.any():
+        i = np.unravel_index(np.argmax(bad), bad.shape)
+        raise AssertionError(f"{name}: {int(bad.sum())}/{bad.size} out of tolerance; first at {i}: "
+                             f"got {got[i]!r} oracle {want[i]!r} fp64 {exact[i]!r}")
+    return int((~ok_oracle & ok_exact).sum())
+
+
+def random_case_n4(i: int):
+    """n = 4 batches large enough for the persistent kernels (T > 128):
+    widths that are multiples of 256 (strip path) or of 64 only (fused)."""
+    c = random_case(1000 + i)
+    rng = c["rng"]
+    D = (256 if i % 2 == 0 else 64) * int(rng.integers(1, 31 if i % 2 == 0 else 124))
+    K = 4 * D
+    t_max = max(129, min(16_000_000 // K, 6000))
+    c.update(n=4, D=D, T=int(rng.integers(129, t_max + 1)),
+             force=str(rng.choice(["split", "fused", "rows", "strip"])))
+    return c
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_shape_parity(pkg, orc, device, i):
+    _run_case(pkg, orc, device, i, random_case(i))
+
+
+@pytest.mark.parametrize("i", range(N_CASES_N4))
+def test_random_persistent_kernel_shapes(pkg, orc, device, i):
+    _run_case(pkg, orc, device, 1000 + i, random_case_n4(i))
+
+
+def _run_case(pkg, orc, device, i, c):
+    n, D, T, is_bf16, has_gamma, rng = c["n"], c["D"], c["T"], c["is_bf16"], c["has_gamma"], c["rng"]
+    K, M = n * D, n * n + 2 * n
+    xf = rng.standard_normal((T, n, D)).astype(np.float32)
+    xf[rng.random(T) < 0.05] *= 30.0  # a few large rows
+    x = to_bits(xf, is_bf16)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
+    alpha = c["alpha"]
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma, c["norm_eps"], c["hc_eps"])
+    exact = exact_outputs(orc, x, is_bf16, phi, alpha, bias, gamma, c["norm_eps"], c["hc_eps"])
+    paths = []
+    for force in (None, c["force"]):
+        _say(f"[random {i}] T={T} n={n} D={D} bf16={is_bf16} gamma={has_gamma} "
+             f"eps=({c['norm_eps']}, {c['hc_eps']}) force={force}")
+        out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma, c["norm_eps"], c["hc_eps"],
+                      force_path=force)
+        fallback = 0
+        for name, key in (("hPre", "h_pre"), ("hPost", "h_post"), ("hRes", "h_res")):
+            fallback += close_to_oracle_or_exact(name, out[key], ref[key], exact[key])
+        assert_hin(out["h_in"], ref["h_in"], x, is_bf16, out["h_pre"], ref["h_pre"], orc)
+        if fallback:
+            _say(f"[random {i}] {fallback} fp32 outputs held to the fp64 value (oracle off it)")
+        paths.append(out["path"])
+    _say(f"[random {i}] paths {paths[0]} / {paths[1]}")
