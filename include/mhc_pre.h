@@ -232,6 +232,21 @@ MHC_API const char *mhcPreStatusString(int status);
  * writes a static NUL-terminated name to *name. */
 MHC_API int mhcPreExecutorPath(const mhcPreExecutor *executor, const char **name);
 
+/*
+ * Measurement aid, no counterpart in the reference: enqueues one launch of a
+ * stream kernel that reads `readBytes` from `src` and writes `writeBytes` to
+ * `dst` with no arithmetic, in the access pattern the device serves best
+ * (whole 1 KB wavefront loads and stores, 4 KB read blocks, grid-strided).
+ * Timing it gives a measured bandwidth ceiling for a byte mix, e.g. the
+ * operator's x read and hIn write, to set beside the operator's own rate.
+ * readBytes must be a multiple of 4096 and writeBytes of 1024 (otherwise
+ * MHC_STATUS_INVALID_SHAPE); src and dst 16-byte aligned.  `workgroups`
+ * workgroups of 512 threads, 0 for one per compute unit.  The written data is
+ * a function of the read data and has no other meaning.
+ */
+MHC_API int mhcPreStreamProbe(const void *src, uint64_t readBytes, void *dst, uint64_t writeBytes,
+                              int32_t workgroups, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

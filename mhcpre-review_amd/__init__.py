@@ -24,6 +24,7 @@ from .binding import (  # noqa: F401
     load_library,
     make_tensor,
     mhc_pre,
+    stream_probe,
 )
 
 

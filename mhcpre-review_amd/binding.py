@@ -107,6 +107,9 @@ def load_library() -> ctypes.CDLL:
     lib.mhcPreGetWorkspaceSizePrepared.argtypes = [T, w, T, T, ctypes.c_float, ctypes.c_float,
                                                    T, T, T, T, P(ctypes.c_uint64), P(exe)]
     lib.mhcPreGetWorkspaceSizePrepared.restype = ctypes.c_int
+    lib.mhcPreStreamProbe.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                                      ctypes.c_uint64, ctypes.c_int32, ctypes.c_void_p]
+    lib.mhcPreStreamProbe.restype = ctypes.c_int
     _LIB = lib
     return lib
 
@@ -365,6 +368,26 @@ class MhcPreOp:
 
     def outputs(self):
         return self.h_in, self.h_post, self.h_res, self.h_pre
+
+
+def stream_probe(src, read_bytes: int, dst, write_bytes: int, workgroups: int = 0,
+                 stream=None) -> None:
+    """Enqueue one launch of the library's stream probe (mhcPreStreamProbe):
+    reads `read_bytes` of the device tensor `src` and writes `write_bytes` of
+    `dst` in the best-served access pattern, with no arithmetic.  A
+    measurement aid: timing it gives a bandwidth ceiling for a byte mix."""
+    import torch
+
+    lib = load_library()
+    if read_bytes > src.numel() * src.element_size() or write_bytes > dst.numel() * dst.element_size():
+        raise ValueError("stream_probe: byte counts exceed the tensors")
+    with torch.cuda.device(src.device):
+        st = lib.mhcPreStreamProbe(ctypes.c_void_p(src.data_ptr()), ctypes.c_uint64(read_bytes),
+                                   ctypes.c_void_p(dst.data_ptr()), ctypes.c_uint64(write_bytes),
+                                   ctypes.c_int32(workgroups),
+                                   ctypes.c_void_p(_stream_handle(stream)))
+    if st != 0:
+        raise MhcPreError("mhcPreStreamProbe", st)
 
 
 def mhc_pre(x, phi, alpha, bias, gamma=None, norm_eps: float = 1e-6, hc_eps: float = 1e-6,

@@ -898,4 +898,36 @@ int mhcPreExecutorPath(const mhcPreExecutor *executor, const char **name)
     return MHC_STATUS_SUCCESS;
 }
 
+int mhcPreStreamProbe(const void *src, uint64_t readBytes, void *dst, uint64_t writeBytes,
+                      int32_t workgroups, hipStream_t stream)
+{
+    if ((readBytes > 0 && src == nullptr) || (writeBytes > 0 && dst == nullptr)) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    if (readBytes % 4096 != 0 || writeBytes % 1024 != 0 || readBytes >= (uint64_t{1} << 42) ||
+        writeBytes >= (uint64_t{1} << 40) || workgroups < 0 || workgroups > 65536) {
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 != 0) {
+        return MHC_STATUS_MISALIGNED;
+    }
+    if (readBytes == 0 && writeBytes == 0) {
+        return MHC_STATUS_SUCCESS;
+    }
+    int wg = workgroups;
+    if (wg == 0) {
+        int device = 0;
+        hipDeviceProp_t prop;
+        if (hipGetDevice(&device) != hipSuccess || hipGetDeviceProperties(&prop, device) != hipSuccess) {
+            return MHC_STATUS_HIP_ERROR;
+        }
+        wg = prop.multiProcessorCount;
+    }
+    (void)hipGetLastError();  // a stale error from an earlier call is not this launch's
+    return mhc::launch_stream_probe(src, static_cast<int64_t>(readBytes), dst, static_cast<int64_t>(writeBytes), wg,
+                                    stream) == hipSuccess
+               ? MHC_STATUS_SUCCESS
+               : MHC_STATUS_HIP_ERROR;
+}
+
 }  // extern "C"

@@ -159,6 +159,12 @@ int rows_gemm_threads();
 int rows_small_rows(int n);
 int rows_small_ksteps();
 
+// Stream probe (mhc_pre_stream.hip): reads readBytes (a multiple of 4096) from
+// src and writes writeBytes (a multiple of 1024) to dst in the best-served
+// access pattern, with `workgroups` workgroups of 512 threads.
+hipError_t launch_stream_probe(const void *src, int64_t readBytes, void *dst, int64_t writeBytes,
+                               int workgroups, hipStream_t stream);
+
 // Workgroups of the strip kernel that can be resident per CU (x numCUs), or
 // -1 if the plan has no strip kernel.
 int strip_max_coresident(const Plan &plan, int numCUs);

@@ -280,3 +280,20 @@ def test_no_alloc_rejects_workspaces_beyond_the_builtin_scratch(pkg, lib):
         lib.mhcPreExecutorDestroy(exe)
     assert lib.mhcPreNoAlloc(None, None) == code(pkg, "MHC_STATUS_NULL_ARGUMENT")
     assert lib.mhcPreStatusString(code(pkg, "MHC_STATUS_SCRATCH_TOO_SMALL")) != b"unknown status"
+
+
+def test_stream_probe_rejects_bad_arguments_before_any_launch(pkg, lib):
+    """mhcPreStreamProbe (a measurement aid) validates before it touches the
+    device: NULL buffers with nonzero sizes, sizes off the block granularity,
+    misaligned buffers and out-of-range grids are refused, and an empty
+    request succeeds without a launch."""
+    probe = lib.mhcPreStreamProbe
+    vp = ctypes.c_void_p
+    assert probe(None, 4096, vp(FAKE), 1024, 0, None) == code(pkg, "MHC_STATUS_NULL_ARGUMENT")
+    assert probe(vp(FAKE), 4096, None, 1024, 0, None) == code(pkg, "MHC_STATUS_NULL_ARGUMENT")
+    assert probe(vp(FAKE), 4000, vp(FAKE), 1024, 0, None) == code(pkg, "MHC_STATUS_INVALID_SHAPE")
+    assert probe(vp(FAKE), 4096, vp(FAKE), 1000, 0, None) == code(pkg, "MHC_STATUS_INVALID_SHAPE")
+    assert probe(vp(FAKE), 4096, vp(FAKE), 1024, -1, None) == code(pkg, "MHC_STATUS_INVALID_SHAPE")
+    assert probe(vp(FAKE), 4096, vp(FAKE), 1024, 70000, None) == code(pkg, "MHC_STATUS_INVALID_SHAPE")
+    assert probe(vp(FAKE + 4), 4096, vp(FAKE), 1024, 0, None) == code(pkg, "MHC_STATUS_MISALIGNED")
+    assert probe(None, 0, None, 0, 0, None) == code(pkg, "MHC_STATUS_SUCCESS")
