@@ -357,19 +357,32 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
     }
     if (n == 4) {
-        // Small n = 4 batches (T <= 128) take the rows path: the persistent
-        // kernels' fixed cost (every workgroup builds its B slice, a team
-        // works through its few tiles one after another) exceeds the rows
-        // path's two or three short launches there (measured on MI355X:
-        // 15-17 us against 19 us at D = 4096 and 7168, 12 us against 27 us at
-        // D = 256).  From T = 512 on the strip kernel is faster.
+        // Small n = 4 batches (T <= 128) of narrow rows take the rows path:
+        // the strip kernel's fixed cost (every workgroup builds its B slice)
+        // is ~12 us whatever the shape, while the rows path's short launches
+        // grow with K.  Measured on MI355X (back to back, bf16, gamma on):
+        // rows 9-14 us against strip 11.5-13 us up to D = 5120; from
+        // D = 5632 the strip kernel is faster at every T (D = 7168: 12.5-13
+        // us against 13-18 us).  The fused and split paths are slower than
+        // rows at these sizes.
         p.path = p.stripP > 0 ? mhc::Path::kStrip
                               : (p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit);
-        if (p.rowsS > 0 && T <= 128) {
+        if (p.rowsS > 0 && T <= 128 && (p.stripP == 0 || D < 5632)) {
             p.path = mhc::Path::kRows;
         }
     } else {
         p.path = p.rowsS > 0 ? mhc::Path::kRows : mhc::Path::kSplit;
+        // Short rows (K <= 12288) and a few hundred to two thousand rows: the
+        // rows path has few row blocks to spread (256 rows each) and many
+        // partial sums per row to add, and the split path's 16-row tiles are
+        // faster.  Measured on MI355X, back to back and after a cache flush:
+        // n = 6, D = 1024, T = 1024: 18.9 / 26.6 us against 36.4 / 40.6 us;
+        // n = 8, D = 1024, T = 1024: 28.4 / 36.9 us against 42.3 / 45.1 us.
+        // Outside that window the rows path is as fast or faster.
+        if (p.path == mhc::Path::kRows && !p.rowsSmall && T >= 256 &&
+            ((K <= 8192 && T <= 2048) || (K <= 12288 && T >= 512 && T <= 1024))) {
+            p.path = mhc::Path::kSplit;
+        }
     }
     if (const char *force = std::getenv("MHCPRE_FORCE_PATH")) {
         if (std::strcmp(force, "split") == 0) {
@@ -544,8 +557,15 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
     if (p.path == mhc::Path::kStrip) {
         // One workgroup per CU, all co-resident; each XCD's CUs hold at least
         // one team of stripP slice workgroups and one reducer workgroup.
+        // Teams of two or more slices get at least two reducers: with one,
+        // the reducer paces the team (measured on MI355X at T = 8192: 43 ->
+        // 32 us at D = 1024, 74 -> 54 us at D = 2304); a single-slice team
+        // keeps one, which leaves room for more teams.
         const int perXcd = shape.cus / shape.xcds;
-        int teamsPerXcd = perXcd / (p.stripP + 1);
+        int teamsPerXcd = perXcd / (p.stripP + (p.stripP >= 2 ? 2 : 1));
+        if (teamsPerXcd < 1) {
+            teamsPerXcd = perXcd / (p.stripP + 1);
+        }
         // Teams beyond the rings' capacity would have no slots of their own
         // (teams without tiles write nothing).
         if (teamsPerXcd * shape.xcds > p.stripMaxTeams && p.stripMaxTeams < p.fusedTiles) {

@@ -338,7 +338,8 @@ def test_shared_workspace_back_to_back(pkg, orc, device, force, expect, n, T, D)
 ])
 def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     """Row-block path (n = 6, 8): ragged row blocks, several K-ranges, fp16 and
-    bf16 x, gamma on and off, against the oracle."""
+    bf16 x, gamma on and off, against the oracle.  The path is forced: the
+    plan takes the split path for some of these shapes."""
     rng = np.random.default_rng(T * 17 + n * 5 + D)
     K, M = n * D, n * n + 2 * n
     xf = rng.standard_normal((T, n, D)).astype(np.float32)
@@ -349,7 +350,7 @@ def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
     gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
     _say(f"[rows] T={T} n={n} D={D} bf16={is_bf16} gamma={has_gamma}")
-    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma, force_path="rows")
     assert out["path"] == "rows"
     ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
     check(out, ref, x, is_bf16, orc)

@@ -161,7 +161,8 @@ def _check_oracle(orc, host, outs, bf16):
     (300, 4, 512, True, True, "split", "split"),
     (77, 6, 48, True, True, None, "split"),
     (77, 6, 256, False, True, None, "rows"),      # n = 6 small-batch GEMM
-    (600, 8, 1024, True, True, None, "rows"),
+    (600, 8, 1024, True, True, "rows", "rows"),  # the plan takes split here
+    (600, 8, 1024, True, True, None, "split"),
     (300, 6, 2048, False, True, None, "rows"),
     (40, 8, 4096, True, True, None, "rows"),      # small-batch GEMM
     (100, 4, 256, False, False, None, "rows"),    # n = 4 small batch
