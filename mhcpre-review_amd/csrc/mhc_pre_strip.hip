@@ -550,6 +550,10 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     __shared__ __attribute__((aligned(16))) float part[kGroups][2][kStrips][RC::COLS * kColPitch];
     // B operand of each strip, in MFMA fragment order (24 KB per strip).
     __shared__ u32x4_t bsh[kStrips][KS][NT][64];
+    // Second staging area of the B build (rows of 256 values of K padded to
+    // kStagePitch bytes, hi then lo).
+    constexpr int kStagePitch = kSlice * 2 + 16;
+    __shared__ __attribute__((aligned(16))) char stage2[kPrep ? 16 : 2 * M * kStagePitch];
     // Per-group count of partials written (4 per own step).
     __shared__ uint32_t arrived[kGroups];
     // The launch's exchange epoch, handed from thread 0 to every wave.
@@ -738,19 +742,20 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     }
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (!kPrep) {  // (prepared fragments were copied above)
-        // One round per stream s, through a staging area in the partials
-        // buffer (idle until the first step): each wave writes its columns'
-        // products gamma * phi as bf16 hi and lo rows (row j: the slice's 256
-        // values of K, padded to kStagePitch bytes so that the 8 lanes of a
-        // read phase hit distinct banks), then builds 3 of the stream's 24
-        // fragments (4 strips x 2 k-steps x NT tiles) from them.
-        constexpr int kStagePitch = kSlice * 2 + 16;
+        // One round per stream s, through two staging areas used in turn
+        // (the partials buffer, idle until the first step, and stage2): each
+        // wave writes its columns' products gamma * phi as bf16 hi and lo
+        // rows (row j: the slice's 256 values of K, padded to kStagePitch
+        // bytes so that the 8 lanes of a read phase hit distinct banks), then
+        // builds 3 of the stream's 24 fragments (4 strips x 2 k-steps x NT
+        // tiles) from them.  Round s + 1's rows are written while round s's
+        // fragments are read, so the rounds take one barrier each.
         static_assert(2 * M * kStagePitch <= (int)sizeof(part), "staging fits the partials buffer");
         static_assert(kStrips * 2 * NT == 3 * kWaves, "fragments per wave and round");
-        char *stHi = reinterpret_cast<char *>(&part[0][0][0][0]);
-        char *stLo = stHi + M * kStagePitch;
-#pragma unroll
-        for (int s = 0; s < N; ++s) {
+        char *const areas[2] = {reinterpret_cast<char *>(&part[0][0][0][0]), stage2};
+        auto write_rows = [&](int s) __attribute__((always_inline)) {
+            char *stHi = areas[s & 1];
+            char *stLo = stHi + M * kStagePitch;
 #pragma unroll
             for (int c = 0; c < CPW; ++c) {
                 float bv[4];
@@ -768,7 +773,16 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 *reinterpret_cast<uint2 *>(stHi + off) = make_uint2(h0, h1);
                 *reinterpret_cast<uint2 *>(stLo + off) = make_uint2(l0, l1);
             }
-            lds_barrier();
+        };
+        write_rows(0);
+        lds_barrier();
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+            if (s + 1 < N) {
+                write_rows(s + 1);  // the other area: its last reader was round s - 1
+            }
+            const char *stHi = areas[s & 1];
+            const char *stLo = stHi + M * kStagePitch;
 #pragma unroll
             for (int f0 = 0; f0 < 3; ++f0) {
                 const int f = 3 * w + f0;  // (strip, q, t) = (f / (2 NT), (f / NT) % 2, f % NT)
@@ -783,7 +797,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                     *reinterpret_cast<const u32x4_t *>((lo ? stLo : stHi) + jc * kStagePitch + 2 * k);
             }
             if (s + 1 < N) {
-                lds_barrier();  // the staging rows are rewritten by the next round
+                lds_barrier();  // round s + 1's rows written, round s's area free again
             }
         }
     }
