@@ -343,6 +343,14 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             }
         }
         p.rowsBlocks = static_cast<int>(blocks);
+        p.rowsBFromPhi = blocks <= mhc::kRowsPhiMaxBlocks;
+        if (const char *phiEnv = std::getenv("MHCPRE_ROWS_B")) {
+            if (std::strcmp(phiEnv, "phi") == 0) {
+                p.rowsBFromPhi = true;
+            } else if (std::strcmp(phiEnv, "prep") == 0) {
+                p.rowsBFromPhi = false;
+            }
+        }
         // Small batches: one K-range per workgroup of the small-batch GEMM,
         // which builds B from phi itself (each element of B is used once).
         const int64_t smallKs = mhc::rows_small_ksteps();
@@ -439,8 +447,11 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     size_t rowsEnd = 0;
     if (p.rowsS > 0) {
         p.wsRowsB = mhc::kWsHeaderBytes;
-        p.wsRowsPartial =
-            align_up(p.wsRowsB + static_cast<size_t>(K / 32) * static_cast<size_t>(p.NT) * 1024, 256);
+        p.wsRowsPartial = p.wsRowsB;
+        if (!p.rowsSmall && !p.rowsBFromPhi) {
+            p.wsRowsPartial =
+                align_up(p.wsRowsB + static_cast<size_t>(K / 32) * static_cast<size_t>(p.NT) * 1024, 256);
+        }
         rowsEnd = align_up(p.wsRowsPartial + static_cast<size_t>(p.rowsS) * static_cast<size_t>(T) *
                                                  static_cast<size_t>(M + 1) * 4,
                            256);

@@ -92,6 +92,9 @@ struct Plan {
     // rows_block_rows() rows.
     int rowsS = 0;
     int rowsBlocks = 0;
+    // The block GEMM builds B from phi and gamma itself (no prep launch);
+    // otherwise a prep kernel writes B fragments to the workspace first.
+    bool rowsBFromPhi = false;
     // Small batches (T <= rows_small_rows(n)): one GEMM workgroup per K-range
     // of rows_small_ksteps() k-steps, B built from phi in registers, no prep.
     bool rowsSmall = false;
@@ -102,7 +105,7 @@ struct Plan {
     size_t wsPartial = 0;     // split: [S][T][M+1] partials
     size_t wsFinal = 0;       // fused: per-tile hPre / invRms blocks (tagged words)
     size_t wsFusedPartial = 0;// fused: per-(tile, slice) exchange records (tagged words)
-    size_t wsRowsB = 0;       // rows: B fragments [K/32][NT][64 lanes] x 16 bytes
+    size_t wsRowsB = 0;       // rows (prep launch): B fragments [K/32][NT][64 lanes] x 16 bytes
     size_t wsRowsPartial = 0; // rows: [rowsS][T][M+1] partials
     size_t wsTotal = 0;
 
@@ -150,6 +153,9 @@ hipError_t launch_prepare_b(int n, const float *phi, const float *gamma, void *b
 // Rows path (mhc_pre_rows.hip); nXcd: XCDs of the device (work placement
 // only).
 hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, hipStream_t stream);
+// Row blocks up to which the block GEMM builds B from phi itself (see
+// mhc_pre_rows.hip); above it a prep launch writes B fragments first.
+constexpr int64_t kRowsPhiMaxBlocks = 16;
 // Rows per work item, k-steps per stage and work-items per workgroup of the
 // rows-path GEMM.
 int rows_block_rows();

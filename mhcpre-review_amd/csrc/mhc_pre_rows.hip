@@ -8,25 +8,22 @@
 // the row's x.  Keeping x on chip until hPre is known (as the persistent n = 4
 // kernels do) would move more bytes between CUs than it saves; so this path
 // runs a split-K GEMM that reads x once, and a second pass that reads x again
-// for hIn.  Three launches:
+// for hIn.  Two launches:
 //
-//   rows_prep_b    B fragments in the order the MFMA reads them:
-//                  [K/32 k-steps][NT tiles][64 lanes] x 16 bytes.  Tile t < Q
-//                  holds hi of columns 16t + l%16 and tile Q + t their lo, in
-//                  the same lanes; when M % 16 == 8 the last tile holds hi
-//                  (lanes 0-7 of each 16) and lo (lanes 8-15) of the last 8
-//                  columns.  Lane l holds k = 32ks + 8(l/16) .. +8.
 //   rows_gemm      split-K GEMM over work items (256-row block, K-range).  A
 //                  workgroup is 8 waves of 32 rows (two 16-row MFMA blocks).
-//                  K is cut into stages of 4 k-steps (two 128-byte lines of a
+//                  K is cut into stages of 2 k-steps (one 128-byte line of a
 //                  row); K-range kr takes a contiguous run of stages.  x is
 //                  read with nontemporal loads (measured on MI355X: 6.4 TB/s
 //                  for this read pattern against 4.9 with default caching or
-//                  with the ranges' stages interleaved).  Each stage's B fragments
-//                  go through registers into an LDS ring (each wave copies
-//                  NT/2 of the 4*NT fragments), its x into a register ring as
-//                  whole 128-byte lines (8 lanes per row), both kAhead stages
-//                  ahead of the MFMAs.  A DPP row_ror:8 turns two
+//                  with the ranges' stages interleaved).  Each stage's B goes
+//                  through registers into an LDS ring: built from phi and
+//                  gamma (256-byte runs of every mix column, split into bf16
+//                  hi + lo rows), or copied from prepared weights (fragments
+//                  in the order the MFMA reads them, as rows_prep_b writes
+//                  them); its x goes into a register ring as whole 128-byte
+//                  lines (8 lanes per row), both kAhead stages ahead of the
+//                  MFMAs.  A DPP row_ror:8 turns two
 //                  line registers into the A fragments of two k-steps.  hi and
 //                  lo products accumulate into one fp32 accumulator per mix
 //                  column; a Gram MFMA of the same fragments gives the sum of
@@ -38,11 +35,17 @@
 //                  read of x with round-half-even stores
 //                  (code/op_kernel/mhc_pre.cpp:761-826).
 //
+// rows_prep_b (mhcPrePrepareWeights) writes the prepared fragments:
+// [K/32 k-steps][NT tiles][64 lanes] x 16 bytes.  Tile t < Q holds hi of
+// columns 16t + l%16 and tile Q + t their lo, in the same lanes; when
+// M % 16 == 8 the last tile holds hi (lanes 0-7 of each 16) and lo (lanes
+// 8-15) of the last 8 columns.  Lane l holds k = 32ks + 8(l/16) .. +8.
+//
 // Work items map to XCDs so that the workgroups of one XCD share K-ranges:
 // workgroup g runs on XCD g mod X (round-robin dispatch) and takes item
 // (g mod X) * C + g / X of the X*C item slots, items numbered row block
-// fastest.  The B fragments of an item's K-range are then read by the other
-// row blocks of the same K-range from that XCD's L2.  The mapping affects
+// fastest.  The phi runs (or prepared fragments) of an item's K-range are then
+// read by the other row blocks of the same K-range from that XCD's L2.  The mapping affects
 // speed only.
 
 #include "mhc_pre_device.h"
@@ -227,7 +230,9 @@ __global__ __launch_bounds__(256) void rows_prep_b_kernel(const float *__restric
 // ---------------------------------------------------------------------------
 struct RowsGemmArgs {
     const uint16_t *x;
-    const u32x4_t *bfrag;
+    const u32x4_t *bfrag;   // prepared B fragments (kPhi false)
+    const float *phi;       // phi [M][K] and gamma [K] or null (kPhi true)
+    const float *gamma;
     float *partial;  // [S][T][M + 1]
     int64_t T;
     int64_t K;
@@ -238,7 +243,19 @@ struct RowsGemmArgs {
     int nXcd;
 };
 
-template <int N, bool kBf16>
+// kPhi: B of each stage is built here from phi and gamma (bit-identical to
+// rows_prep_b's fragments: the same product and splits), so a launch needs no
+// prep kernel.  The workgroup loads the stage's 64 values of K of every mix
+// column as 256-byte runs (16 lanes per column, 4 values per lane, whole
+// lines), multiplies by gamma, splits into bf16 hi and lo and writes them as
+// rows of an LDS block: row j (hi of column j) and row M + j (its lo), each
+// 64 values padded to kPhiPitch bytes, so that the 16 lanes of a fragment
+// read phase (16 rows, pitch 144 bytes) hit distinct banks.  The MFMAs then
+// read their fragments from those rows.  Without kPhi the stage's fragments
+// come from the prepared buffer in fragment order.
+constexpr int kPhiPitch = kStageKs * 32 * 2 + 16;
+
+template <int N, bool kBf16, bool kPhi>
 __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
 {
     using C = RowsCols<N>;
@@ -249,10 +266,14 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
     constexpr int kLines = kStageKs / 2;      // 128-byte lines of a row per stage
     constexpr int SF = kStageKs * NT;         // B fragments per stage
     constexpr int NB = (SF + kRW - 1) / kRW;  // fragments each wave copies (some waves one fewer)
+    constexpr int NP = (16 * M + kRW * kWave - 1) / (kRW * kWave);  // phi loads per lane and stage
     constexpr int kXLoads = 4 * kLines;       // x line loads per wave and stage
+    constexpr int kBLoads = kPhi ? NP + 1 : NB;  // B loads per wave and stage (phi runs + gamma)
     constexpr int kUnroll = kXSlots;          // steps per loop trip: every ring index static
     static_assert(kUnroll % kBSets == 0 && kUnroll % 2 == 0, "static ring indices");
-    __shared__ u32x4_t bsh[2][SF][kWave];     // B of stages s and s + 1
+    static_assert(kStageKs == 2, "a stage is 64 values of K: 16 lanes x 4 per mix column");
+    constexpr int kStageBytes = kPhi ? 2 * M * kPhiPitch : SF * kWave * 16;
+    __shared__ __attribute__((aligned(16))) char bsh[2][kStageBytes];  // B of stages s and s + 1
 
     const int lane = threadIdx.x & 63;
     // Wave-uniform (scalar) wave index: the buffer resources built from it
@@ -276,10 +297,17 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
     const int K2 = (int)(a.K * 2);  // row stride in bytes
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + (vrows > 0 ? r0 * a.K : 0), vrows * K2);
     const int xLane = (lane & 7) * K2 + 2 * (8 * (lane >> 4) + 32 * ((lane >> 3) & 1));
-    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bfrag, a.NS * SF * kWave * 16);
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(a.bfrag, kPhi ? 0 : a.NS * SF * kWave * 16);
+    const bool hasGamma = a.gamma != nullptr;
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.phi, kPhi ? M * K2 * 2 : 0);
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gamma, kPhi && hasGamma ? K2 * 2 : 0);
+    // kPhi: lane l of wave w loads, with its i-th phi load, the 4 values of K
+    // at 4 (l & 15) of mix column pj(i) = 32 i + 4 w + (l >> 4) (none past M).
+    const int pk = 4 * (lane & 15);
+    auto pj = [&](int i) { return 32 * i + 4 * w + (lane >> 4); };
 
     u32x4_t xs[kXSlots][4][kLines];  // [slot][8-row group][line of the stage]
-    u32x4_t bst[kBSets][NB];         // B fragments of a stage on their way to LDS
+    u32x4_t bst[kBSets][kBLoads];    // B of a stage on its way to LDS
 
     // Per-lane offsets are loop-invariant registers and the stage's part of
     // each address is a scalar offset.
@@ -295,15 +323,26 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
     // loads in the same order, live or not: stages past the K-range (and a
     // wave's fragment slots past SF) read through size-0 resources, so the
     // counter waits below stay exact.
-    auto issue = [&](int s, u32x4_t(&bd)[NB], u32x4_t(&xd)[4][kLines]) {
+    auto issue = [&](int s, u32x4_t(&bd)[kBLoads], u32x4_t(&xd)[4][kLines]) {
         const bool live = s < nst;
         const int gs = gs0 + s;  // stage of K
+        if constexpr (kPhi) {
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const int fr = w + kRW * i;
-            const __amdgpu_buffer_rsrc_t bq = (live && fr < SF) ? br : make_rsrc(a.bfrag, 0);
-            bd[i] = __builtin_bit_cast(
-                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(bq, bLane, (gs * SF + kRW * i) * (kWave * 16), 0));
+            for (int i = 0; i < NP; ++i) {
+                const __amdgpu_buffer_rsrc_t pq = (live && 32 * i + 4 * w < M) ? pr : make_rsrc(a.phi, 0);
+                bd[i] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(pq, (pj(i) * (K2 / 2) + pk) * 4, gs * 256, 0));
+            }
+            bd[NP] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(live ? gr : make_rsrc(a.gamma, 0), pk * 4, gs * 256, 0));
+        } else {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int fr = w + kRW * i;
+                const __amdgpu_buffer_rsrc_t bq = (live && fr < SF) ? br : make_rsrc(a.bfrag, 0);
+                bd[i] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(bq, bLane, (gs * SF + kRW * i) * (kWave * 16), 0));
+            }
         }
         // Keep the B loads ahead of the x lines in the (in-order) load
         // counter: waiting for them must not wait for this stage's x.
@@ -321,14 +360,52 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
         // Stages stay in issue order in the load counter.
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto stash = [&](int sl, const u32x4_t(&bd)[NB]) {
+    auto stash = [&](int sl, const u32x4_t(&bd)[kBLoads]) {
+        if constexpr (kPhi) {
+            const f32x4_t gv = __builtin_bit_cast(f32x4_t, bd[NP]);
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            const int fr = w + kRW * i;
-            if (fr < SF) {
-                bsh[sl][fr][lane] = bd[i];
+            for (int i = 0; i < NP; ++i) {
+                if (32 * i + 4 * w < M) {  // (wave-uniform)
+                    f32x4_t bv = __builtin_bit_cast(f32x4_t, bd[i]);
+                    if (hasGamma) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            bv[e] = bv[e] * gv[e];
+                        }
+                    }
+                    uint32_t h0, l0, h1, l1;  // bf16(B) and bf16(B - hi) of k pairs (pk, pk+1), (pk+2, pk+3)
+                    split2_bf16(bv[0], bv[1], h0, l0);
+                    split2_bf16(bv[2], bv[3], h1, l1);
+                    char *row = &bsh[sl][pj(i) * kPhiPitch + 2 * pk];
+                    *reinterpret_cast<uint2 *>(row) = make_uint2(h0, h1);
+                    *reinterpret_cast<uint2 *>(row + M * kPhiPitch) = make_uint2(l0, l1);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int fr = w + kRW * i;
+                if (fr < SF) {
+                    reinterpret_cast<u32x4_t *>(bsh[sl])[fr * kWave + lane] = bd[i];
+                }
             }
         }
+    };
+    // kPhi: the byte offset in a stage block of lane `lane`'s fragment of
+    // tile t, k-step 0 (k-step ksl adds 64 bytes): tile t < Q holds hi of
+    // columns 16 t + l % 16 (rows 16 t + l % 16), tile Q + t their lo (rows
+    // M + ...); when M % 16 == 8, tile 2Q holds hi (lanes l % 16 < 8) and lo
+    // (the others) of columns 16 Q + l % 8.  Lane l holds k = 8 (l / 16) ...
+    const int fragBase = (lane & 15) * kPhiPitch + 16 * (lane >> 4);
+    const int halfBase = (((lane & 15) < 8 ? 0 : M) + 16 * Q + (lane & 7)) * kPhiPitch + 16 * (lane >> 4);
+    auto frag_off = [&](int t) {
+        if (t < Q) {
+            return fragBase + 16 * t * kPhiPitch;
+        }
+        if (t < 2 * Q) {
+            return fragBase + (M + 16 * (t - Q)) * kPhiPitch;
+        }
+        return halfBase;
     };
 
     f32x4_t acc[2][NA];
@@ -366,7 +443,7 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
         const int s = s0 + u;
         const int sl = u % kXSlots;
         const int bl = u % 2;
-        wait_vm<kXLoads + (kAhead - 2) * (NB + kXLoads)>();
+        wait_vm<kXLoads + (kAhead - 2) * (kBLoads + kXLoads)>();
         lds_barrier();
         stash((u + 1) % 2, bst[(u + 1) % kBSets]);
         issue(s + kAhead, bst[(u + kAhead) % kBSets], xs[(u + kAhead) % kXSlots]);
@@ -378,7 +455,11 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
             for (int ksl = 0; ksl < kStageKs; ++ksl) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    bf[ksl][t] = bsh[bl][ksl * NT + t][lane];
+                    if constexpr (kPhi) {
+                        bf[ksl][t] = *reinterpret_cast<const u32x4_t *>(&bsh[bl][frag_off(t) + 64 * ksl]);
+                    } else {
+                        bf[ksl][t] = reinterpret_cast<const u32x4_t *>(bsh[bl])[(ksl * NT + t) * kWave + lane];
+                    }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -939,7 +1020,6 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
 {
     char *ws = static_cast<char *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(ws);
-    u32x4_t *bfrag = reinterpret_cast<u32x4_t *>(ws + p.wsRowsB);
     float *partial = reinterpret_cast<float *>(ws + p.wsRowsPartial);
     using C = RowsCols<N>;
     hipError_t err = hipSuccess;
@@ -963,7 +1043,12 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
                                dim3(kSmallWaves * 64), 0, stream, sa);
         }
     } else {
-        if (bprep == nullptr) {
+        // Without prepared weights the GEMM builds each stage's B from phi
+        // and gamma itself (rowsBFromPhi) or reads fragments a prep launch
+        // wrote to the workspace.
+        u32x4_t *bfrag = reinterpret_cast<u32x4_t *>(ws + p.wsRowsB);
+        const bool fromPhi = bprep == nullptr && p.rowsBFromPhi;
+        if (bprep == nullptr && !fromPhi) {
             const int64_t prepThreads = (p.K / 32) * C::NA * kWave;
             hipLaunchKernelGGL((rows_prep_b_kernel<N>), dim3((unsigned)((prepThreads + 255) / 256)),
                                dim3(256), 0, stream, p.phi, p.hasGamma ? p.gamma : nullptr, bfrag, p.K,
@@ -976,6 +1061,8 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
         RowsGemmArgs g;
         g.x = static_cast<const uint16_t *>(p.x);
         g.bfrag = bprep != nullptr ? bprep : bfrag;
+        g.phi = p.phi;
+        g.gamma = p.hasGamma ? p.gamma : nullptr;
         g.partial = partial;
         g.T = p.T;
         g.K = p.K;
@@ -985,8 +1072,13 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
         g.nXcd = nXcd;
         const int items = p.rowsBlocks * p.rowsS;
         g.perXcd = (items + nXcd - 1) / nXcd;
-        hipLaunchKernelGGL((rows_gemm_kernel<N, kBf16>), dim3((unsigned)(g.perXcd * nXcd)),
-                           dim3(kRW * 64), 0, stream, g);
+        if (!fromPhi) {
+            hipLaunchKernelGGL((rows_gemm_kernel<N, kBf16, false>), dim3((unsigned)(g.perXcd * nXcd)),
+                               dim3(kRW * 64), 0, stream, g);
+        } else {
+            hipLaunchKernelGGL((rows_gemm_kernel<N, kBf16, true>), dim3((unsigned)(g.perXcd * nXcd)),
+                               dim3(kRW * 64), 0, stream, g);
+        }
     }
     err = hipGetLastError();
     if (err != hipSuccess) {

@@ -119,16 +119,19 @@ def _bits(t):
     return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
 
 
-def _run(pkg, x, phi, alpha, bias, gamma, weights=None, force=None):
+def _run(pkg, x, phi, alpha, bias, gamma, weights=None, force=None, rows_b=None):
     import torch
 
     if force:
         os.environ["MHCPRE_FORCE_PATH"] = force
+    if rows_b:
+        os.environ["MHCPRE_ROWS_B"] = rows_b
     try:
         op = pkg.MhcPreOp(x, None if weights else phi, alpha, bias, None if weights else gamma,
                           h_pre=True, weights=weights)
     finally:
         os.environ.pop("MHCPRE_FORCE_PATH", None)
+        os.environ.pop("MHCPRE_ROWS_B", None)
     op.launch()
     torch.cuda.synchronize()
     assert op.device_status() == 0
@@ -180,6 +183,37 @@ def test_prepared_matches_plain(pkg, orc, device, T, n, D, bf16, gamma_on, force
     for a, b, name in zip(p_outs, plain, ("hIn", "hPost", "hRes", "hPre")):
         assert torch.equal(_bits(a), _bits(b)), name
     _check_oracle(orc, host, p_outs, bf16)
+    w.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,n,D,bf16,gamma_on,force", [
+    (600, 8, 1024, True, True, "rows"),
+    (300, 6, 2048, False, True, None),
+    (1000, 4, 1024, True, True, "rows"),     # n = 4: the half tile of M = 24
+    (700, 4, 768, False, False, "rows"),
+    (4200, 8, 512, False, False, "rows"),    # 17 row blocks: the plan's prep launch
+    (520, 8, 2048, True, True, None),
+])
+def test_rows_gemm_b_sources_match(pkg, orc, device, T, n, D, bf16, gamma_on, force):
+    """The block GEMM's two plain B sources -- built from phi in the GEMM
+    (MHCPRE_ROWS_B=phi) or read from fragments a prep launch wrote (=prep) --
+    and prepared weights give bit-identical outputs, which match the oracle."""
+    import torch
+
+    host, (x, phi, alpha, bias, gamma) = _case(device, T, n, D, bf16, gamma_on, seed=3 * T + D)
+    _say(f"[rows B] T={T} n={n} D={D} bf16={bf16} gamma={gamma_on} force={force}")
+    outs = {}
+    for src in ("phi", "prep"):
+        path, outs[src] = _run(pkg, x, phi, alpha, bias, gamma, force=force, rows_b=src)
+        assert path == "rows"
+    w = pkg.MhcPreWeights(phi, gamma, n)
+    path, outs["prepared"] = _run(pkg, x, phi, alpha, bias, gamma, weights=w, force=force)
+    assert path == "rows"
+    for src in ("prep", "prepared"):
+        for a, b, name in zip(outs["phi"], outs[src], ("hIn", "hPost", "hRes", "hPre")):
+            assert torch.equal(_bits(a), _bits(b)), (src, name)
+    _check_oracle(orc, host, outs["phi"], bf16)
     w.close()
 
 
