@@ -220,6 +220,9 @@ def main() -> int:
     ap.add_argument("--settle-ms", type=float, default=100.0,
                     help="wall time of back-to-back launches before the warm-up (clock settling)")
     ap.add_argument("--config", type=int, default=3, choices=sorted(WORKLOADS))
+    ap.add_argument("--shape", type=str, default=None,
+                    help="n,D,T,bf16,gamma (e.g. 8,8192,2048,1,1): another workload in place of "
+                         "--config, with the same input distributions (seed of config 0)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target duration of the CPU-baseline sample (0 disables it)")
     ap.add_argument("--prepared", action="store_true",
@@ -242,8 +245,16 @@ def main() -> int:
         print("no GPU visible", file=sys.stderr)
         return 1
     device = torch.device("cuda:0")
-    n, D, T, bf16, gamma_on, _ = WORKLOADS[args.config]
-    x, phi, alpha, bias, gamma = make_inputs(args.config, device)
+    cfg = args.config
+    if args.shape is not None:
+        parts = [int(v) for v in args.shape.split(",")]
+        if len(parts) != 5:
+            print("--shape takes n,D,T,bf16,gamma", file=sys.stderr)
+            return 2
+        cfg = 0
+        WORKLOADS[cfg] = (parts[0], parts[1], parts[2], bool(parts[3]), bool(parts[4]), False)
+    n, D, T, bf16, gamma_on, _ = WORKLOADS[cfg]
+    x, phi, alpha, bias, gamma = make_inputs(cfg, device)
     weights = None
     if args.prepared:
         # B = gamma * phi prepared once, outside the timed region (the
