@@ -156,6 +156,9 @@ hipError_t launch_rows(const Plan &plan, void *workspace, int nXcd, hipStream_t 
 // Row blocks up to which the block GEMM builds B from phi itself (see
 // mhc_pre_rows.hip); above it a prep launch writes B fragments first.
 constexpr int64_t kRowsPhiMaxBlocks = 16;
+// Whether the rows-path epilogue of `rows` rows over S K-ranges runs its
+// 1024-thread variant (mhc_pre_rows.hip).
+bool rows_epilogue_wide(int n, int S, int64_t rows);
 // Rows per work item, k-steps per stage and work-items per workgroup of the
 // rows-path GEMM.
 int rows_block_rows();

@@ -890,17 +890,17 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         const int64_t stride = a.T * COLS;
         float v = 0.f;
         if constexpr (kEpiThreads >= 1024) {
-            // Many K-ranges (this variant is taken when a group would have
-            // more than 8 partials): up to 32 are loaded before the first add
+            // Small batches with many K-ranges (this variant's use is set by
+            // rows_epilogue_wide): up to 32 are loaded before the first add
             // (one memory round trip, where a load per add costs one each),
-            // then added in K-range order.  Slots past the group's range
-            // re-read its last partial and are not added.
+            // then added in K-range order.  Slots past the group's range load
+            // nothing.
             constexpr int kBatch = 32;
             for (int sk = sBeg; sk < sEnd; sk += kBatch) {
                 float t[kBatch];
 #pragma unroll
                 for (int i = 0; i < kBatch; ++i) {
-                    t[i] = src[(int64_t)min(sk + i, sEnd - 1) * stride];
+                    t[i] = sk + i < sEnd ? src[(int64_t)(sk + i) * stride] : 0.f;
                 }
 #pragma unroll
                 for (int i = 0; i < kBatch; ++i) {
@@ -1100,13 +1100,10 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
     e.normEps = p.normEps;
     e.hcEps = p.hcEps;
     e.invFlatDim = p.invFlatDim;
-    // Many K-ranges: more threads share each row's sums once a 256-thread
-    // group would add more than 8 partials per column.
-    constexpr int kCols = C::M + 1;
-    const bool wide = (p.rowsS + 256 / kCols - 1) / (256 / kCols) > 8;
     for (int64_t r0 = 0; r0 < p.T; r0 += kEpilogueRowsPerLaunch) {
         e.row0 = r0;
         const int64_t rows = std::min<int64_t>(kEpilogueRowsPerLaunch, p.T - r0);
+        const bool wide = rows_epilogue_wide(N, p.rowsS, rows);
         // Fewer rows than a wave of workgroups (small batches): each row's
         // hIn is split over up to 8 workgroups of at least 128 column octets
         // each, so that more CUs share the x reads (each part sums the row's
@@ -1160,6 +1157,25 @@ hipError_t launch_prepare_b(int n, const float *phi, const float *gamma, void *b
                            static_cast<uint32_t *>(nullptr));
     }
     return hipGetLastError();
+}
+
+// The epilogue's 1024-thread variant (12 groups of M + 1 threads at n = 8
+// sum the K-range partials, one octet of x per thread) against the 256-thread
+// one (3 groups, four octets per thread).  With few rows the partial sums are
+// a large part of a row's work and more threads in flight win; from a few
+// hundred rows on, x dominates and the 256-thread workgroups stream it faster.
+// Measured on MI355X (us per launch back to back, 1024 / 256 threads): n = 8,
+// D = 7168, T = 64 (224 K-ranges) 16.7 / 20.2; n = 8, D = 8192, T = 256 30.1 /
+// 32.1; n = 4, D = 4096, T = 128 12.3 / 13.8; n = 6, D = 1024, T = 64 10.1 /
+// 10.9; n = 4, D = 256, T = 128 (4 K-ranges) 12.4 / 11.8; n = 8, D = 8192,
+// T = 512 43.7 / 43.1, T = 2048 129.1 / 123.1; n = 6, D = 4096, T = 512 28.9 /
+// 26.2.  So: the 1024-thread variant for at most 256 rows when a 256-thread
+// group would add at least 4 partials per column.
+bool rows_epilogue_wide(int n, int S, int64_t rows)
+{
+    const int cols = n * n + 2 * n + 1;
+    const int perGroup = (S + 256 / cols - 1) / (256 / cols);
+    return rows <= 256 && perGroup >= 4;
 }
 
 int rows_block_rows() { return kRowBlock; }
