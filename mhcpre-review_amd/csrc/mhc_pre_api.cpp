@@ -365,30 +365,34 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
     }
     if (n == 4) {
-        // Small n = 4 batches (T <= 128) of narrow rows take the rows path:
-        // the strip kernel's fixed cost (every workgroup builds its B slice)
-        // is ~12 us whatever the shape, while the rows path's short launches
-        // grow with K.  Measured on MI355X (back to back, bf16, gamma on):
-        // rows 9-14 us against strip 11.5-13 us up to D = 5120; from
-        // D = 5632 the strip kernel is faster at every T (D = 7168: 12.5-13
-        // us against 13-18 us).  The fused and split paths are slower than
-        // rows at these sizes.
+        // Small n = 4 batches take the rows path: the strip kernel's fixed
+        // cost (every workgroup builds its B slice) is ~12 us whatever the
+        // shape, while the rows path's two short launches grow with K and T.
+        // Measured on MI355X (back to back, bf16, gamma on, rows / strip):
+        // T <= 64 rows at every width (D = 7168: T = 16 10.7 / 12.4, T = 64
+        // 11.7 / 12.8; D = 5632, T = 64 11.3 / 11.8); T = 128 and 160 rows
+        // below D = 5632 (D = 4096, T = 160 12.2 / 12.7; D = 5120, T = 160
+        // 12.0 / 13.3) and strip from there (D = 5632, T = 128 12.6 / 12.3;
+        // D = 7168, T = 160 13.8 / 13.4); T = 256 strip (D = 4096 15.2 /
+        // 12.6).  The fused and split paths are slower than both here.
         p.path = p.stripP > 0 ? mhc::Path::kStrip
                               : (p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit);
-        if (p.rowsS > 0 && T <= 128 && (p.stripP == 0 || D < 5632)) {
+        if (p.rowsS > 0 && (T <= 64 || (T <= 160 && (p.stripP == 0 || D < 5632)))) {
             p.path = mhc::Path::kRows;
         }
     } else {
         p.path = p.rowsS > 0 ? mhc::Path::kRows : mhc::Path::kSplit;
-        // Short rows (K <= 12288) and a few hundred to two thousand rows: the
-        // rows path has few row blocks to spread (256 rows each) and many
-        // partial sums per row to add, and the split path's 16-row tiles are
-        // faster.  Measured on MI355X, back to back and after a cache flush:
-        // n = 6, D = 1024, T = 1024: 18.9 / 26.6 us against 36.4 / 40.6 us;
-        // n = 8, D = 1024, T = 1024: 28.4 / 36.9 us against 42.3 / 45.1 us.
-        // Outside that window the rows path is as fast or faster.
-        if (p.path == mhc::Path::kRows && !p.rowsSmall && T >= 256 &&
-            ((K <= 8192 && T <= 2048) || (K <= 12288 && T >= 512 && T <= 1024))) {
+        // Short rows (K <= 12288) and one to two thousand rows: the rows path
+        // has few row blocks to spread (256 rows each) and many partial sums
+        // per row to add, and the split path's 16-row tiles are faster.
+        // Measured on MI355X, back to back (rows / split, us): n = 6, D =
+        // 1024: T = 256 12.8 / 14.6, 512 15.2 / 16.0, 1024 23.2 / 18.9, 2048
+        // 35.2 / 25.9; n = 6, D = 2048: T = 512 20.5 / 22.6, 1024 30.5 /
+        // 28.9, 2048 41.6 / 40.2; n = 8, D = 1024: T = 256 15.7 / 19.0, 512
+        // 22.4 / 20.6, 1024 31.8 / 28.1, 2048 40.6 / 40.2; n = 8, D = 512,
+        // T = 1024 25.3 / 17.6; n = 8, D = 2048 (K = 16384) rows at every T.
+        if (p.path == mhc::Path::kRows && !p.rowsSmall && K <= 12288 && T <= 2048 &&
+            (T >= 1024 || (T >= 512 && n == 8 && K <= 8192))) {
             p.path = mhc::Path::kSplit;
         }
     }

@@ -237,22 +237,32 @@ def _path(pkg, lib, d, env=None):
     (4, 7168, 4096, "strip"),  # D % 256 == 0, D / 256 <= 31
     (4, 64, 4096, "fused"),    # n = 4, D % 64 == 0, not a strip shape
     (4, 48, 64, "split"),      # n = 4, D % 64 != 0
-    (4, 5120, 128, "rows"),    # small n = 4 batch (T <= 128) below D = 5632, K % 128 == 0
+    (4, 5120, 128, "rows"),    # small n = 4 batch (T <= 160) below D = 5632, K % 128 == 0
     (4, 256, 128, "rows"),
-    (4, 7168, 128, "strip"),   # small batch, D >= 5632: the strip kernel
-    (4, 5632, 1, "strip"),
+    (4, 4096, 160, "rows"),
+    (4, 4096, 161, "strip"),
+    (4, 7168, 128, "strip"),   # D >= 5632: the strip kernel above T = 64
+    (4, 7168, 65, "strip"),
+    (4, 7168, 64, "rows"),     # T <= 64: rows at every width
+    (4, 5632, 1, "rows"),
     (4, 7168, 129, "strip"),
     (4, 5696, 64, "rows"),     # D >= 5632 but not a strip width: rows, not fused
     (8, 7168, 64, "rows"),     # n = 8, K % 128 == 0
     (8, 8192, 5472, "rows"),
     (6, 1024, 16, "rows"),     # K = 6144
-    (6, 1024, 2048, "split"),  # K <= 8192, 256 <= T <= 2048
+    (6, 1024, 2048, "split"),  # K <= 12288, 1024 <= T <= 2048
+    (6, 1024, 1024, "split"),
+    (6, 1024, 512, "rows"),
     (8, 1024, 1024, "split"),
-    (8, 1024, 255, "rows"),
+    (8, 1024, 512, "split"),   # n = 8, K <= 8192: from T = 512
+    (8, 1024, 511, "rows"),
+    (8, 1024, 256, "rows"),
     (8, 1024, 2049, "rows"),
-    (6, 2048, 512, "split"),   # K = 12288, 512 <= T <= 1024
-    (6, 2048, 2048, "rows"),
+    (6, 2048, 512, "rows"),    # K = 12288: from T = 1024
+    (6, 2048, 1024, "split"),
+    (6, 2048, 2048, "split"),
     (8, 1536, 1024, "split"),
+    (8, 1536, 512, "rows"),
     (8, 2048, 1024, "rows"),   # K = 16384
     (6, 48, 16, "split"),      # K = 288: not a multiple of 128
     (8, 16, 16, "rows"),       # K = 128
