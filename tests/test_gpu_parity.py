@@ -183,6 +183,10 @@ def test_audit_formula_cases(pkg, orc, device, case):
     (333, 4, 7168, True, True),
     (49, 4, 1792, False, False),
     (1000, 4, 64, True, True),
+    (64, 4, 7168, True, True),     # decode batch at the headline width: the rows path
+    (16, 4, 7936, False, True),
+    (160, 4, 5120, True, False),   # n = 4, T = 160: the rows path's block GEMM
+    (300, 8, 1024, True, True),    # below the split window: the rows path
 ])
 def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     rng = np.random.default_rng(T * 131 + n * 7 + D)
