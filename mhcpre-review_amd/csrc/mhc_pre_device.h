@@ -148,6 +148,13 @@ __device__ __forceinline__ void wait_all_memory()
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// The value of lane l ^ 8 within each row of 16 lanes (DPP row_ror:8): a VALU
+// move, where a shuffle would take an LDS round trip and a wait.
+__device__ __forceinline__ float row_swap8(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t &v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 __device__ __forceinline__ f32x4_t mfma16(const u32x4_t &a, const u32x4_t &b, const f32x4_t &c)

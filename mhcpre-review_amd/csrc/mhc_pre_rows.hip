@@ -549,7 +549,7 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
             if constexpr (C::kHalf) {
                 // hi in lanes 0-7 of each 16, lo of the same column 8 lanes up.
                 const float v = acc[r][Q][e];
-                const float lo = __shfl_down(v, 8, 16);
+                const float lo = row_swap8(v);
                 if (ok && (lane & 15) < 8) {
                     drow[16 * Q + (lane & 7)] = v + lo;
                 }
@@ -563,14 +563,13 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// rows_small: decode-shaped batches (T <= 64).  One workgroup per K-range of
-// kSmallWaves * kSmallKs k-steps; each wave takes kSmallKs of them for all T
-// rows (four 16-row blocks, rows past T read as zeros) and builds its B
-// fragments from phi and gamma in registers, so no prepared copy of B is
-// written or read: with one row block, every element of B is used once.
-// With prepared weights (kPrep) it loads its fragments from the prepared
-// buffer instead.  The waves' partial sums meet in LDS and are added in wave
-// order.
+// rows_small: decode-shaped batches (T <= small_rows(n)).  One workgroup per
+// K-range of kSmallWaves * kSmallKs k-steps.  Each wave builds the B
+// fragments of kSmallKs of them from phi and gamma (or copies them from the
+// prepared buffer) into LDS; after one barrier every wave multiplies its own
+// 16-row blocks by all of the K-range's fragments and writes its rows'
+// partial sums from registers.  Rows past T read as zeros and are not
+// written; a wave whose blocks all start at or past T skips the products.
 // ---------------------------------------------------------------------------
 struct RowsSmallArgs {
     const uint16_t *x;
@@ -589,60 +588,73 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     using C = RowsCols<N>;
     constexpr int M = C::M;
     constexpr int NA = C::NA;
+    constexpr int NT = C::NT;
     constexpr int Q = C::Q;
     constexpr int COLS = M + 1;
-    constexpr int kSmallRows = small_rows<N>();
-    constexpr int RB = kSmallRows / 16;
-    // LDS: each wave's phi block, staged in row order (row pitch kPhiPitch
-    // floats: consecutive rows start 4 banks apart), then, after a barrier,
-    // the waves' sums.
-    constexpr int kPhiK = kSmallKs * 32;   // phi columns (k) per wave
+    constexpr int kKs = kSmallWaves * kSmallKs;          // k-steps per workgroup
+    constexpr int RBW = small_rows<N>() / 16 / kSmallWaves;  // row blocks per wave
+    static_assert(kSmallKs == 2, "one 128-byte line of each row per k-step pair");
+    static_assert(RBW >= 1, "every wave holds at least one row block");
+    // LDS: one region per wave.  It first holds the wave's phi block in row
+    // order (row pitch kPhiPitch floats: consecutive rows start 4 banks
+    // apart), which the wave reads back in B-fragment order, then the
+    // wave's fragments [kSmallKs][NT][64 lanes] (hi tiles, lo tiles, then
+    // the half tile), in the order of the prepared buffer.
+    constexpr int kPhiK = kSmallKs * 32;
     constexpr int kPhiPitch = kPhiK + 4;
-    constexpr int kRedFloats = kSmallWaves * kSmallRows * COLS;
-    constexpr int kStageFloats = kSmallWaves * M * kPhiPitch;
-    __shared__ __attribute__((aligned(16))) float lds[kRedFloats > kStageFloats ? kRedFloats : kStageFloats];
-    float(*red)[kSmallRows][COLS] = reinterpret_cast<float(*)[kSmallRows][COLS]>(lds);
+    constexpr int kStageBytes = M * kPhiPitch * 4;
+    constexpr int kFragBytes = kSmallKs * NT * kWave * 16;
+    constexpr int kRegion = kStageBytes > kFragBytes ? kStageBytes : kFragBytes;
+    __shared__ __attribute__((aligned(16))) char lds[kSmallWaves * kRegion];
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float *stage = lds + w * (M * kPhiPitch);
+    char *const region = lds + w * kRegion;
+    float *const stage = reinterpret_cast<float *>(region);
+    u32x4_t *const frags = reinterpret_cast<u32x4_t *>(region);
     const int kr = blockIdx.x;
     const int T = (int)a.T;
     if (kr == 0 && threadIdx.x == 0) {
         *a.status = kDeviceOk;
     }
     const int K2 = (int)(a.K * 2);
-    const int64_t ks0 = ((int64_t)kr * kSmallWaves + w) * kSmallKs;  // first k-step of this wave
+    const int64_t kg0 = (int64_t)kr * kKs;            // first k-step of the workgroup
+    const int64_t ks0 = kg0 + (int64_t)w * kSmallKs;  // first k-step this wave builds
 
-    // x as whole 128-byte lines (the wave's two k-steps of a row): register
-    // (r, h) holds, in lane l, row 16r + 8h + (l & 7) and the 8 k at
-    // 8(l >> 4) + 32((l >> 3) & 1); a DPP exchange turns each pair into the
-    // A fragments of the two k-steps.
-    static_assert(kSmallKs == 2, "one 128-byte line of each row per wave");
+    // x as whole 128-byte lines (two k-steps of a row): for pair p, register
+    // (i, p, h) holds, in lane l, row 16(w RBW + i) + 8h + (l & 7) and the 8
+    // k at 8(l >> 4) + 32((l >> 3) & 1) of k-steps kg0 + 2p and kg0 + 2p + 1;
+    // a DPP exchange turns each pair into the A fragments of the two.
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, T * K2);
-    u32x4_t xln[RB][2];
+    constexpr int kPairs = kKs / 2;
+    u32x4_t xln[RBW][kPairs][2];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
+    for (int i = 0; i < RBW; ++i) {
+        const int rowBase = 16 * (w * RBW + i);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            xln[r][h] = load16<kCpolNt>(xr, (16 * r + 8 * h + (lane & 7)) * K2 + (int)(ks0 * 64) +
-                                                16 * (lane >> 4) + 64 * ((lane >> 3) & 1));
+        for (int p = 0; p < kPairs; ++p) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                xln[i][p][h] = load16<kCpolNt>(xr, (rowBase + 8 * h + (lane & 7)) * K2 +
+                                                       (int)((kg0 + 2 * p) * 64) + 16 * (lane >> 4) +
+                                                       64 * ((lane >> 3) & 1));
+            }
         }
     }
     // phi rows as whole 256-byte runs (the wave's 64 k of 4 rows per load),
     // into LDS in row order; read back below in B-fragment order.  Prepared
-    // weights: the wave's NT fragments of each k-step instead.
+    // weights: the wave's NT fragments of each of its k-steps instead.
     constexpr int kPhiLoads = kPrep ? 1 : M / 4;
     static_assert(M % 4 == 0, "4 phi rows per load");
     f32x4_t phl[kPhiLoads];
     f32x4_t gm[kSmallKs][2];
-    u32x4_t pf[kSmallKs][kPrep ? C::NT : 1];
+    u32x4_t pf[kSmallKs][kPrep ? NT : 1];
     if constexpr (kPrep) {
 #pragma unroll
         for (int kk = 0; kk < kSmallKs; ++kk) {
 #pragma unroll
-            for (int t = 0; t < C::NT; ++t) {
-                pf[kk][t] = a.bprep[((ks0 + kk) * C::NT + t) * kWave + lane];
+            for (int t = 0; t < NT; ++t) {
+                pf[kk][t] = a.bprep[((ks0 + kk) * NT + t) * kWave + lane];
             }
         }
     } else {
@@ -662,22 +674,24 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     // Every load is issued before any use: one memory round trip.
     __builtin_amdgcn_sched_barrier(0);
 
-    if constexpr (!kPrep) {
+    if constexpr (kPrep) {
+#pragma unroll
+        for (int kk = 0; kk < kSmallKs; ++kk) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                frags[(kk * NT + t) * kWave + lane] = pf[kk][t];
+            }
+        }
+    } else {
 #pragma unroll
         for (int i = 0; i < kPhiLoads; ++i) {
             *reinterpret_cast<f32x4_t *>(stage + (4 * i + (lane >> 4)) * kPhiPitch + 4 * (lane & 15)) = phl[i];
         }
-    }
-    u32x4_t xa[kSmallKs][RB];
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-        lines_to_frags(xln[r][0], xln[r][1], xa[0][r], xa[1][r]);
-    }
-    // B-fragment order: accumulator tile ta covers mix columns 16ta + (l & 15);
-    // the half tile's lanes 8-15 hold the lo half of the column of lanes 0-7.
-    // (The wave reads only its own staging block, which it wrote above.)
-    f32x4_t ph[kSmallKs][NA][2];
-    if constexpr (!kPrep) {
+        // B-fragment order: tile ta covers mix columns 16ta + (l & 15); the
+        // half tile's lanes 8-15 hold the lo half of the column of lanes 0-7.
+        // (The wave reads only its own region, which it wrote above, and
+        // overwrites it with its fragments once every read has returned.)
+        f32x4_t ph[kSmallKs][NA][2];
 #pragma unroll
         for (int kk = 0; kk < kSmallKs; ++kk) {
 #pragma unroll
@@ -688,39 +702,12 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
                 ph[kk][ta][1] = *reinterpret_cast<const f32x4_t *>(src + 4);
             }
         }
-    }
-
-    f32x4_t acc[RB][NA];
-    f32x4_t gram[RB];
+        const bool hasGamma = a.gamma != nullptr;
+        u32x4_t fr[kSmallKs][NT];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-        gram[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < kSmallKs; ++kk) {
 #pragma unroll
-        for (int t = 0; t < NA; ++t) {
-            acc[r][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    const bool hasGamma = a.gamma != nullptr;
-#pragma unroll
-    for (int kk = 0; kk < kSmallKs; ++kk) {
-        u32x4_t xh[RB], xl[RB];
-        if constexpr (!kBf16) {
-#pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                float fx[8];
-                unpack8<false>(xa[kk][r], fx);
-                split_f16_to_bf16(fx, xh[r], xl[r]);
-            }
-        }
-#pragma unroll
-        for (int ta = 0; ta < NA; ++ta) {
-            u32x4_t bh, bl;
-            if constexpr (kPrep) {
-                // Tile ta holds hi of its columns, tile Q + ta their lo; the
-                // half tile (ta == Q) is hi and lo in one fragment.
-                bh = pf[kk][ta < Q ? ta : 2 * Q];
-                bl = pf[kk][ta < Q ? Q + ta : 2 * Q];
-            } else {
+            for (int ta = 0; ta < NA; ++ta) {
                 float b[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -729,87 +716,137 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
                         b[e] = b[e] * gm[kk][e >> 2][e & 3];
                     }
                 }
+                u32x4_t bh, bl;
 #pragma unroll
-                for (int w = 0; w < 4; ++w) {
+                for (int q = 0; q < 4; ++q) {
                     uint32_t h, l;
-                    split2_bf16(b[2 * w], b[2 * w + 1], h, l);
-                    bh[w] = h;
-                    bl[w] = l;
+                    split2_bf16(b[2 * q], b[2 * q + 1], h, l);
+                    bh[q] = h;
+                    bl[q] = l;
                 }
-            }
-            if (ta < Q) {
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    if constexpr (kBf16) {
-                        acc[r][ta] = mfma16(xa[kk][r], bh, acc[r][ta]);
-                        acc[r][ta] = mfma16(xa[kk][r], bl, acc[r][ta]);
-                    } else {
-                        acc[r][ta] = mfma16(xh[r], bh, acc[r][ta]);
-                        acc[r][ta] = mfma16(xh[r], bl, acc[r][ta]);
-                        acc[r][ta] = mfma16(xl[r], bh, acc[r][ta]);
-                    }
-                }
-            } else {
-                // Half tile: hi in lanes 0-7 of each 16, lo in lanes 8-15
-                // (a prepared fragment holds them so already).
-                const u32x4_t bq = kPrep ? bh : ((lane & 15) < 8 ? bh : bl);
-#pragma unroll
-                for (int r = 0; r < RB; ++r) {
-                    if constexpr (kBf16) {
-                        acc[r][ta] = mfma16(xa[kk][r], bq, acc[r][ta]);
-                    } else {
-                        acc[r][ta] = mfma16(xh[r], bq, acc[r][ta]);
-                        acc[r][ta] = mfma16(xl[r], bq, acc[r][ta]);
-                    }
+                if (ta < Q) {
+                    fr[kk][ta] = bh;
+                    fr[kk][Q + ta] = bl;
+                } else if constexpr (C::kHalf) {
+                    // Half tile: hi in lanes 0-7 of each 16, lo in lanes 8-15.
+                    fr[kk][2 * Q] = (lane & 15) < 8 ? bh : bl;
                 }
             }
         }
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
+        for (int kk = 0; kk < kSmallKs; ++kk) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                frags[(kk * NT + t) * kWave + lane] = fr[kk][t];
+            }
+        }
+    }
+    lds_barrier();
+
+    // Row blocks of this wave that hold rows below T (wave-uniform).
+    const int live = min(RBW, max(0, (T - 16 * w * RBW + 15) / 16));
+    if (live == 0) {
+        return;
+    }
+    u32x4_t xa[kKs][RBW];
+#pragma unroll
+    for (int i = 0; i < RBW; ++i) {
+#pragma unroll
+        for (int p = 0; p < kPairs; ++p) {
+            lines_to_frags(xln[i][p][0], xln[i][p][1], xa[2 * p][i], xa[2 * p + 1][i]);
+        }
+    }
+    f32x4_t acc[RBW][NA];
+    f32x4_t gram[RBW];
+#pragma unroll
+    for (int i = 0; i < RBW; ++i) {
+        gram[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < NA; ++t) {
+            acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    // k-steps in order: k-step kk's fragments were built by wave kk / kSmallKs.
+#pragma unroll
+    for (int kk = 0; kk < kKs; ++kk) {
+        const u32x4_t *src = reinterpret_cast<const u32x4_t *>(lds + (kk / kSmallKs) * kRegion) +
+                             (kk % kSmallKs) * NT * kWave + lane;
+        u32x4_t bf[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            bf[t] = src[t * kWave];
+        }
+#pragma unroll
+        for (int i = 0; i < RBW; ++i) {
+            if (i >= live) {
+                continue;
+            }
+            u32x4_t xh, xl;
+            if constexpr (!kBf16) {
+                float fx[8];
+                unpack8<false>(xa[kk][i], fx);
+                split_f16_to_bf16(fx, xh, xl);
+            }
+#pragma unroll
+            for (int t = 0; t < Q; ++t) {
+                if constexpr (kBf16) {
+                    acc[i][t] = mfma16(xa[kk][i], bf[t], acc[i][t]);
+                    acc[i][t] = mfma16(xa[kk][i], bf[Q + t], acc[i][t]);
+                } else {
+                    acc[i][t] = mfma16(xh, bf[t], acc[i][t]);
+                    acc[i][t] = mfma16(xh, bf[Q + t], acc[i][t]);
+                    acc[i][t] = mfma16(xl, bf[t], acc[i][t]);
+                }
+            }
+            if constexpr (C::kHalf) {
+                if constexpr (kBf16) {
+                    acc[i][Q] = mfma16(xa[kk][i], bf[2 * Q], acc[i][Q]);
+                } else {
+                    acc[i][Q] = mfma16(xh, bf[2 * Q], acc[i][Q]);
+                    acc[i][Q] = mfma16(xl, bf[2 * Q], acc[i][Q]);
+                }
+            }
             if constexpr (kBf16) {
-                gram[r] = mfma16(xa[kk][r], xa[kk][r], gram[r]);
+                gram[i] = mfma16(xa[kk][i], xa[kk][i], gram[i]);
             } else {
-                gram[r] = mfma16_f16(xa[kk][r], xa[kk][r], gram[r]);
+                gram[i] = mfma16_f16(xa[kk][i], xa[kk][i], gram[i]);
             }
         }
     }
 
-    // Every wave has read its phi block: the LDS now takes the sums.
-    __syncthreads();
-    // This wave's sums into LDS (C fragment: lane l, register e holds row
-    // 4(l >> 4) + e, column l & 15 of its tile).
+    // Partial sums of this wave's rows (C fragment: lane l, register e holds
+    // row 4(l >> 4) + e, column l & 15 of its tile); read once, by the
+    // epilogue.
+    float *dst = a.partial + (int64_t)kr * a.T * COLS;
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
+    for (int i = 0; i < RBW; ++i) {
+        if (i >= live) {
+            continue;
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int row = 16 * r + 4 * (lane >> 4) + e;
+            const int row = 16 * (w * RBW + i) + 4 * (lane >> 4) + e;
+            const bool ok = row < T;
+            float *drow = dst + (int64_t)row * COLS;
 #pragma unroll
             for (int t = 0; t < Q; ++t) {
-                red[w][row][16 * t + (lane & 15)] = acc[r][t][e];
-            }
-            if constexpr (C::kHalf) {
-                const float v = acc[r][Q][e];
-                const float lo = __shfl_down(v, 8, 16);
-                if ((lane & 15) < 8) {
-                    red[w][row][16 * Q + (lane & 7)] = v + lo;
+                if (ok) {
+                    __builtin_nontemporal_store(acc[i][t][e], &drow[16 * t + (lane & 15)]);
                 }
             }
-            if ((lane & 15) == 4 * (lane >> 4) + e) {
-                red[w][row][M] = gram[r][e];
+            if constexpr (C::kHalf) {
+                // hi in lanes 0-7 of each 16, lo of the same column 8 lanes up.
+                const float v = acc[i][Q][e];
+                const float lo = row_swap8(v);
+                if (ok && (lane & 15) < 8) {
+                    __builtin_nontemporal_store(v + lo, &drow[16 * Q + (lane & 7)]);
+                }
+            }
+            // Diagonal of the Gram tile: the row's sum of squares.
+            if (ok && (lane & 15) == 4 * (lane >> 4) + e) {
+                __builtin_nontemporal_store(gram[i][e], &drow[M]);
             }
         }
-    }
-    __syncthreads();
-    float *dst = a.partial + (int64_t)kr * a.T * COLS;
-    for (int idx = threadIdx.x; idx < T * COLS; idx += kSmallWaves * 64) {
-        const int r = idx / COLS;
-        const int c = idx - r * COLS;
-        float v = red[0][r][c];
-#pragma unroll
-        for (int i = 1; i < kSmallWaves; ++i) {
-            v = v + red[i][r][c];
-        }
-        __builtin_nontemporal_store(v, &dst[idx]);  // read once, by the next kernel
     }
 }
 

@@ -928,6 +928,9 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         if constexpr (!kFull) {
             return;
         }
+        // Ring slot of own tile jj (drain copies, with b >= L, return above;
+        // the clamp keeps their discarded remainder in bounds).
+        constexpr int bx = b < L ? b : 0;
 
         // 2. GEMM of own tile jj (zeros past the last tile) and its Gram
         //    matrix, one stream at a time; after each stream's MFMAs the
@@ -951,7 +954,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
 #pragma unroll
         for (int s = 0; s < N; ++s) {
             u32x4_t kf[2];
-            lines_to_frags(xb[b][s][0], xb[b][s][1], kf[0], kf[1]);
+            lines_to_frags(xb[bx][s][0], xb[bx][s][1], kf[0], kf[1]);
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int ks = 2 * s + q;
