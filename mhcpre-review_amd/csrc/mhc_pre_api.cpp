@@ -365,20 +365,45 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
     }
     if (n == 4) {
-        // Small n = 4 batches take the rows path: the strip kernel's fixed
-        // cost (every workgroup builds its B slice) is ~12 us whatever the
-        // shape, while the rows path's two short launches grow with K and T.
-        // Measured on MI355X (back to back, bf16, gamma on, rows / strip):
-        // T <= 64 rows at every width (D = 7168: T = 16 10.7 / 12.4, T = 64
-        // 11.7 / 12.8; D = 5632, T = 64 11.3 / 11.8); T = 128 and 160 rows
-        // below D = 5632 (D = 4096, T = 160 12.2 / 12.7; D = 5120, T = 160
-        // 12.0 / 13.3) and strip from there (D = 5632, T = 128 12.6 / 12.3;
-        // D = 7168, T = 160 13.8 / 13.4); T = 256 strip (D = 4096 15.2 /
-        // 12.6).  The fused and split paths are slower than both here.
-        p.path = p.stripP > 0 ? mhc::Path::kStrip
-                              : (p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit);
-        if (p.rowsS > 0 && (T <= 64 || (T <= 160 && (p.stripP == 0 || D < 5632)))) {
+        // The strip kernel where it applies (D % 256 == 0), except small
+        // batches: its fixed cost (every workgroup builds its B slice) is
+        // ~12 us whatever the shape, while the rows path's two short
+        // launches grow with K and T.  Measured on MI355X (back to back, us,
+        // bf16 with gamma unless noted, rows / strip): T <= 128 rows at every
+        // width (D = 7168: T = 64 10.4 / 12.2, T = 128 11.8 / 12.4; fp16
+        // without gamma T = 96 11.9 / 12.6, T = 128 12.9 / 12.6, the one
+        // loss); T = 160 rows up to D = 6144 (13.0 / 13.2; D = 7168 13.7 /
+        // 13.5); up to T = 256 rows while T * D <= 2^19 (D = 2048, T = 256
+        // 11.6 / 12.3; D = 3072, T = 192 12.1 / 12.3 and D = 4096, T = 192
+        // 13.3 / 12.9 stay strip); up to T = 1024 while T * D <= 3 * 2^17
+        // (D = 768, T = 512 11.5 / 11.7; D = 256, T = 1024 10.8 / 11.9;
+        // D = 512, T = 1024 12.4 / 11.7 and D = 1024, T = 512 12.5 / 12.3
+        // stay strip).
+        //
+        // Other widths take the rows path, or the split path for short rows
+        // (K <= 8704) from T = 2048, whose 16-row tiles then beat the rows
+        // path's reread of x; the fused kernel was slower than one of the
+        // two at every shape measured (rows / split / fused: D = 7104, T =
+        // 8192 166 / 264 / 754; D = 4160, T = 8192 107 / 144 / 374; D =
+        // 4160, T = 1024 24.1 / 30.7 / 64.7; D = 2112, T = 1024 17.7 / 19.8
+        // / 32.0; D = 2112, T = 8192 68.5 / 66.0 / 131; D = 1216, T = 2048
+        // 21.4 / 19.0 / 29.1; D = 384, T = 4096 24.6 / 15.5 / 25.0; D = 192,
+        // T = 8192 35.2 / 17.5 / 21.5) and stays the fallback of shapes the
+        // rows path cannot hold.
+        if (p.stripP > 0) {
+            p.path = mhc::Path::kStrip;
+            const int64_t td = T * D;
+            if (p.rowsS > 0 && (T <= 128 || (T <= 160 && D <= 6144) || (T <= 256 && td <= (int64_t{1} << 19)) ||
+                                (T <= 1024 && td <= 3 * (int64_t{1} << 17)))) {
+                p.path = mhc::Path::kRows;
+            }
+        } else if (p.rowsS > 0) {
             p.path = mhc::Path::kRows;
+            if (!p.rowsSmall && K <= 8704 && T >= 2048) {
+                p.path = mhc::Path::kSplit;
+            }
+        } else {
+            p.path = p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit;
         }
     } else {
         p.path = p.rowsS > 0 ? mhc::Path::kRows : mhc::Path::kSplit;

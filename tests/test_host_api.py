@@ -235,18 +235,31 @@ def _path(pkg, lib, d, env=None):
 
 @pytest.mark.parametrize("n,D,S,want", [
     (4, 7168, 4096, "strip"),  # D % 256 == 0, D / 256 <= 31
-    (4, 64, 4096, "fused"),    # n = 4, D % 64 == 0, not a strip shape
+    (4, 64, 4096, "split"),    # n = 4, not a strip width: split for K <= 8704 from T = 2048
+    (4, 64, 2047, "rows"),
+    (4, 2176, 2048, "split"),  # K = 8704
+    (4, 2240, 2048, "rows"),   # K = 8960: rows, not fused
+    (4, 7104, 8192, "rows"),
     (4, 48, 64, "split"),      # n = 4, D % 64 != 0
-    (4, 5120, 128, "rows"),    # small n = 4 batch (T <= 160) below D = 5632, K % 128 == 0
+    (4, 5120, 128, "rows"),    # small n = 4 batch: T <= 128 at every width
     (4, 256, 128, "rows"),
-    (4, 4096, 160, "rows"),
-    (4, 4096, 161, "strip"),
-    (4, 7168, 128, "strip"),   # D >= 5632: the strip kernel above T = 64
-    (4, 7168, 65, "strip"),
-    (4, 7168, 64, "rows"),     # T <= 64: rows at every width
+    (4, 7168, 128, "rows"),
+    (4, 7168, 64, "rows"),
     (4, 5632, 1, "rows"),
+    (4, 4096, 160, "rows"),    # T <= 160 up to D = 6144
+    (4, 6144, 160, "rows"),
     (4, 7168, 129, "strip"),
-    (4, 5696, 64, "rows"),     # D >= 5632 but not a strip width: rows, not fused
+    (4, 7168, 160, "strip"),
+    (4, 4096, 161, "strip"),   # T <= 256: rows while T * D <= 2^19
+    (4, 2048, 256, "rows"),
+    (4, 3072, 192, "strip"),
+    (4, 2048, 257, "strip"),   # T <= 1024: rows while T * D <= 3 * 2^17
+    (4, 768, 512, "rows"),
+    (4, 1024, 512, "strip"),
+    (4, 256, 1024, "rows"),
+    (4, 256, 1025, "strip"),
+    (4, 512, 1024, "strip"),
+    (4, 5696, 64, "rows"),     # not a strip width: rows, not fused
     (8, 7168, 64, "rows"),     # n = 8, K % 128 == 0
     (8, 8192, 5472, "rows"),
     (6, 1024, 16, "rows"),     # K = 6144

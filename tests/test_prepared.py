@@ -157,10 +157,12 @@ def _check_oracle(orc, host, outs, bf16):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("T,n,D,bf16,gamma_on,force,path", [
-    (300, 4, 512, True, True, None, "strip"),
-    (300, 4, 512, False, False, None, "strip"),
+    (300, 4, 512, True, True, "strip", "strip"),  # the plan takes rows here
+    (300, 4, 512, False, False, "strip", "strip"),
+    (300, 4, 512, True, True, None, "rows"),       # n = 4, T * D <= 3 * 2^17
     (300, 4, 512, True, True, "fused", "fused"),
-    (200, 4, 192, True, True, None, "fused"),
+    (200, 4, 192, True, True, "fused", "fused"),  # the plan takes rows here
+    (200, 4, 192, False, True, None, "rows"),     # n = 4 width without a strip slice
     (300, 4, 512, True, True, "split", "split"),
     (77, 6, 48, True, True, None, "split"),
     (77, 6, 256, False, True, None, "rows"),      # n = 6 small-batch GEMM
