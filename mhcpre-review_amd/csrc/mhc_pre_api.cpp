@@ -363,6 +363,22 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         if (static_cast<int64_t>(p.rowsS) * T * (M + 1) * 4 >= (int64_t{1} << 31)) {
             p.rowsS = 0;
         }
+        // Many K-ranges: partials row-major, so that each epilogue workgroup
+        // reads its row's sums as one run.  Measured on MI355X (back to back,
+        // us, K-range-major / row-major): n = 8, D = 7168, T = 64 (S = 224)
+        // 16.8 / 16.0; n = 8, D = 8192, T = 256 30.2 / 28.9, T = 2048 123.3 /
+        // 122.0; n = 6, D = 4096, T = 512 26.5 / 24.9; with few K-ranges the
+        // GEMM's scattered short writes cost more (n = 4, D = 256, T = 128,
+        // S = 4: 10.1 / 10.6; n = 8, D = 8192, T = 5472, S = 11: 280.2 /
+        // 282.0).
+        p.rowsRowMajor = p.rowsS >= 32;
+        if (const char *layoutEnv = std::getenv("MHCPRE_ROWS_PARTIALS")) {
+            if (std::strcmp(layoutEnv, "rows") == 0) {
+                p.rowsRowMajor = true;
+            } else if (std::strcmp(layoutEnv, "ranges") == 0) {
+                p.rowsRowMajor = false;
+            }
+        }
     }
     if (n == 4) {
         // The strip kernel where it applies (D % 256 == 0), except small

@@ -98,6 +98,9 @@ struct Plan {
     // Small batches (T <= rows_small_rows(n)): one GEMM workgroup per K-range
     // of rows_small_ksteps() k-steps, B built from phi in registers, no prep.
     bool rowsSmall = false;
+    // Partial sums stored row-major, [T][rowsS][M+1] (each row's sums
+    // contiguous for its epilogue), instead of [rowsS][T][M+1].
+    bool rowsRowMajor = false;
 
     // Workspace layout (byte offsets).  The paths' regions overlap: a
     // workspace holds one launch at a time.
@@ -106,7 +109,7 @@ struct Plan {
     size_t wsFinal = 0;       // fused: per-tile hPre / invRms blocks (tagged words)
     size_t wsFusedPartial = 0;// fused: per-(tile, slice) exchange records (tagged words)
     size_t wsRowsB = 0;       // rows (prep launch): B fragments [K/32][NT][64 lanes] x 16 bytes
-    size_t wsRowsPartial = 0; // rows: [rowsS][T][M+1] partials
+    size_t wsRowsPartial = 0; // rows: partials, [rowsS][T][M+1] or [T][rowsS][M+1]
     size_t wsTotal = 0;
 
     // Bound device pointers (caller memory).

@@ -27,8 +27,10 @@
 //                  line registers into the A fragments of two k-steps.  hi and
 //                  lo products accumulate into one fp32 accumulator per mix
 //                  column; a Gram MFMA of the same fragments gives the sum of
-//                  squares on its diagonal.  Writes partial[K-range][row][M+1]
-//                  (mix columns, then the sum of squares).
+//                  squares on its diagonal.  Writes the M+1 partial sums of
+//                  each (row, K-range) (mix columns, then the sum of squares):
+//                  K-range-major, or row-major when there are many K-ranges
+//                  (each row's sums then one contiguous run for its epilogue).
 //   rows_epilogue  one workgroup per row: the K-range partials summed in
 //                  K-range order, invRms, the sigmoid / affine epilogue
 //                  (code/op_kernel/mhc_pre.cpp:735-758), and hIn from a second
@@ -233,7 +235,9 @@ struct RowsGemmArgs {
     const u32x4_t *bfrag;   // prepared B fragments (kPhi false)
     const float *phi;       // phi [M][K] and gamma [K] or null (kPhi true)
     const float *gamma;
-    float *partial;  // [S][T][M + 1]
+    float *partial;  // element (row, K-range, column) at row * rowStride + kr * rangeStride + column
+    int64_t rowStride;
+    int64_t rangeStride;
     int64_t T;
     int64_t K;
     int NS;          // stages of K (K / 32 / kStageKs)
@@ -532,14 +536,14 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
 
     // C fragment: lane l, register e holds row 4(l >> 4) + e, column l & 15
     // of its 16 x 16 tile.
-    float *dst = a.partial + ((int64_t)kr * a.T + r0) * (M + 1);
+    float *dst = a.partial + (int64_t)r0 * a.rowStride + (int64_t)kr * a.rangeStride;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int row = 16 * r + 4 * (lane >> 4) + e;
             const bool ok = row < vrows;
-            float *drow = dst + (int64_t)row * (M + 1);
+            float *drow = dst + (int64_t)row * a.rowStride;
 #pragma unroll
             for (int t = 0; t < Q; ++t) {
                 if (ok) {
@@ -576,8 +580,10 @@ struct RowsSmallArgs {
     const float *phi;
     const float *gamma;
     const u32x4_t *bprep;  // prepared B fragments [K/32][NT][64] (kPrep only)
-    float *partial;    // [S][T][M + 1]
+    float *partial;    // element (row, K-range, column) at row * rowStride + kr * rangeStride + column
     uint32_t *status;  // low half of the device status word
+    int64_t rowStride;
+    int64_t rangeStride;
     int64_t T;
     int64_t K;
 };
@@ -590,7 +596,6 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     constexpr int NA = C::NA;
     constexpr int NT = C::NT;
     constexpr int Q = C::Q;
-    constexpr int COLS = M + 1;
     constexpr int kKs = kSmallWaves * kSmallKs;          // k-steps per workgroup
     constexpr int RBW = small_rows<N>() / 16 / kSmallWaves;  // row blocks per wave
     static_assert(kSmallKs == 2, "one 128-byte line of each row per k-step pair");
@@ -817,7 +822,7 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     // Partial sums of this wave's rows (C fragment: lane l, register e holds
     // row 4(l >> 4) + e, column l & 15 of its tile); read once, by the
     // epilogue.
-    float *dst = a.partial + (int64_t)kr * a.T * COLS;
+    float *dst = a.partial + (int64_t)kr * a.rangeStride;
 #pragma unroll
     for (int i = 0; i < RBW; ++i) {
         if (i >= live) {
@@ -827,7 +832,7 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
         for (int e = 0; e < 4; ++e) {
             const int row = 16 * (w * RBW + i) + 4 * (lane >> 4) + e;
             const bool ok = row < T;
-            float *drow = dst + (int64_t)row * COLS;
+            float *drow = dst + (int64_t)row * a.rowStride;
 #pragma unroll
             for (int t = 0; t < Q; ++t) {
                 if (ok) {
@@ -857,7 +862,9 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
 // ---------------------------------------------------------------------------
 struct RowsEpiArgs {
     const uint16_t *x;
-    const float *partial;  // [S][T][M + 1]
+    const float *partial;  // element (row, K-range, column) at row * rowStride + kr * rangeStride + column
+    int64_t rowStride;
+    int64_t rangeStride;
     const float *alpha;
     const float *bias;
     uint16_t *hIn;
@@ -923,8 +930,8 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         const int Sg = (a.S + G - 1) / G;
         const int sBeg = q * Sg;
         const int sEnd = min(a.S, sBeg + Sg);
-        const float *src = a.partial + row * COLS + j;
-        const int64_t stride = a.T * COLS;
+        const float *src = a.partial + row * a.rowStride + j;
+        const int64_t stride = a.rangeStride;
         float v = 0.f;
         if constexpr (kEpiThreads >= 1024) {
             // Small batches with many K-ranges (this variant's use is set by
@@ -1058,6 +1065,9 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
     char *ws = static_cast<char *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(ws);
     float *partial = reinterpret_cast<float *>(ws + p.wsRowsPartial);
+    constexpr int64_t kCols = RowsCols<N>::M + 1;
+    const int64_t rowStride = p.rowsRowMajor ? p.rowsS * kCols : kCols;
+    const int64_t rangeStride = p.rowsRowMajor ? kCols : p.T * kCols;
     using C = RowsCols<N>;
     hipError_t err = hipSuccess;
 
@@ -1069,6 +1079,8 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
         sa.gamma = p.hasGamma ? p.gamma : nullptr;
         sa.bprep = bprep;
         sa.partial = partial;
+        sa.rowStride = rowStride;
+        sa.rangeStride = rangeStride;
         sa.status = status;
         sa.T = p.T;
         sa.K = p.K;
@@ -1101,6 +1113,8 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
         g.phi = p.phi;
         g.gamma = p.hasGamma ? p.gamma : nullptr;
         g.partial = partial;
+        g.rowStride = rowStride;
+        g.rangeStride = rangeStride;
         g.T = p.T;
         g.K = p.K;
         g.NS = (int)(p.K / 32 / kStageKs);
@@ -1125,6 +1139,8 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
     RowsEpiArgs e;
     e.x = static_cast<const uint16_t *>(p.x);
     e.partial = partial;
+    e.rowStride = rowStride;
+    e.rangeStride = rangeStride;
     e.alpha = p.alpha;
     e.bias = p.bias;
     e.hIn = static_cast<uint16_t *>(p.hIn);

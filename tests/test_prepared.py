@@ -119,19 +119,22 @@ def _bits(t):
     return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
 
 
-def _run(pkg, x, phi, alpha, bias, gamma, weights=None, force=None, rows_b=None):
+def _run(pkg, x, phi, alpha, bias, gamma, weights=None, force=None, rows_b=None, layout=None):
     import torch
 
     if force:
         os.environ["MHCPRE_FORCE_PATH"] = force
     if rows_b:
         os.environ["MHCPRE_ROWS_B"] = rows_b
+    if layout:
+        os.environ["MHCPRE_ROWS_PARTIALS"] = layout
     try:
         op = pkg.MhcPreOp(x, None if weights else phi, alpha, bias, None if weights else gamma,
                           h_pre=True, weights=weights)
     finally:
         os.environ.pop("MHCPRE_FORCE_PATH", None)
         os.environ.pop("MHCPRE_ROWS_B", None)
+        os.environ.pop("MHCPRE_ROWS_PARTIALS", None)
     op.launch()
     torch.cuda.synchronize()
     assert op.device_status() == 0
@@ -217,6 +220,34 @@ def test_rows_gemm_b_sources_match(pkg, orc, device, T, n, D, bf16, gamma_on, fo
             assert torch.equal(_bits(a), _bits(b)), (src, name)
     _check_oracle(orc, host, outs["phi"], bf16)
     w.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,n,D,bf16,gamma_on,force", [
+    (100, 4, 256, False, False, None),      # small-batch GEMM, 4 K-ranges
+    (40, 8, 4096, True, True, None),        # small-batch GEMM, rows past T in the last block
+    (64, 8, 7168, False, False, None),      # 224 K-ranges: the 1024-thread epilogue in 4 parts
+    (64, 6, 1024, True, True, None),
+    (300, 4, 512, True, True, None),        # block GEMM, B built from phi, the half tile
+    (600, 8, 1024, True, True, "rows"),
+    (4200, 8, 512, False, False, "rows"),   # 17 row blocks: the prep launch
+    (2100, 6, 2048, True, True, None),      # ragged last row block
+])
+def test_rows_partial_layouts_match(pkg, orc, device, T, n, D, bf16, gamma_on, force):
+    """The rows path's partial sums stored K-range-major or row-major
+    (MHCPRE_ROWS_PARTIALS=ranges / rows) give bit-identical outputs: the
+    layout changes addresses only, not the order of any sum."""
+    import torch
+
+    host, (x, phi, alpha, bias, gamma) = _case(device, T, n, D, bf16, gamma_on, seed=5 * T + D + n)
+    _say(f"[rows layout] T={T} n={n} D={D} bf16={bf16} gamma={gamma_on} force={force}")
+    outs = {}
+    for layout in ("ranges", "rows"):
+        path, outs[layout] = _run(pkg, x, phi, alpha, bias, gamma, force=force, layout=layout)
+        assert path == "rows"
+    for a, b, name in zip(outs["ranges"], outs["rows"], ("hIn", "hPost", "hRes", "hPre")):
+        assert torch.equal(_bits(a), _bits(b)), name
+    _check_oracle(orc, host, outs["rows"], bf16)
 
 
 @pytest.mark.gpu
