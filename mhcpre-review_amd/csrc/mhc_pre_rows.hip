@@ -76,7 +76,11 @@ constexpr int kBSets = kAhead - 1;           // B staging register sets
 // per 16 rows, n = 6 and 8 have 3 and 5).
 template <int N>
 constexpr int small_rows() { return N == 4 ? 128 : 64; }
-constexpr int kSmallWaves = 4;               // small-batch GEMM: waves splitting a K-range
+constexpr int kSmallWaves = 4;               // small-batch GEMM: waves building a K-range's B
+// Small-batch GEMM: waves per workgroup, each multiplying its own 16-row
+// blocks (n = 4: 8 waves of one block; n = 6, 8: 4 waves of one block).
+template <int N>
+constexpr int small_waves() { return N == 4 ? 8 : 4; }
 constexpr int kSmallKs = 2;                  // small-batch GEMM: k-steps per wave
 
 // Column tiles of the B operand and the accumulator tile each one adds into.
@@ -568,12 +572,13 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
 
 // ---------------------------------------------------------------------------
 // rows_small: decode-shaped batches (T <= small_rows(n)).  One workgroup per
-// K-range of kSmallWaves * kSmallKs k-steps.  Each wave builds the B
-// fragments of kSmallKs of them from phi and gamma (or copies them from the
-// prepared buffer) into LDS; after one barrier every wave multiplies its own
-// 16-row blocks by all of the K-range's fragments and writes its rows'
-// partial sums from registers.  Rows past T read as zeros and are not
-// written; a wave whose blocks all start at or past T skips the products.
+// K-range of kSmallWaves * kSmallKs k-steps.  Each of the first kSmallWaves
+// waves builds the B fragments of kSmallKs of them from phi and gamma (or
+// copies them from the prepared buffer) into LDS; after one barrier every
+// wave multiplies its own 16-row blocks by all of the K-range's fragments
+// and writes its rows' partial sums from registers.  Rows past T read as
+// zeros and are not written; a wave whose blocks all start at or past T
+// skips the products.
 // ---------------------------------------------------------------------------
 struct RowsSmallArgs {
     const uint16_t *x;
@@ -589,7 +594,7 @@ struct RowsSmallArgs {
 };
 
 template <int N, bool kBf16, bool kPrep>
-__global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallArgs a)
+__global__ __launch_bounds__(small_waves<N>() * 64) void rows_small_kernel(RowsSmallArgs a)
 {
     using C = RowsCols<N>;
     constexpr int M = C::M;
@@ -597,10 +602,11 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     constexpr int NT = C::NT;
     constexpr int Q = C::Q;
     constexpr int kKs = kSmallWaves * kSmallKs;          // k-steps per workgroup
-    constexpr int RBW = small_rows<N>() / 16 / kSmallWaves;  // row blocks per wave
+    constexpr int RBW = small_rows<N>() / 16 / small_waves<N>();  // row blocks per wave
     static_assert(kSmallKs == 2, "one 128-byte line of each row per k-step pair");
     static_assert(RBW >= 1, "every wave holds at least one row block");
-    // LDS: one region per wave.  It first holds the wave's phi block in row
+    static_assert(small_waves<N>() >= kSmallWaves, "every builder wave also multiplies");
+    // LDS: one region per builder wave.  It first holds the wave's phi block in row
     // order (row pitch kPhiPitch floats: consecutive rows start 4 banks
     // apart), which the wave reads back in B-fragment order, then the
     // wave's fragments [kSmallKs][NT][64 lanes] (hi tiles, lo tiles, then
@@ -614,7 +620,9 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    char *const region = lds + w * kRegion;
+    const bool builder = w < kSmallWaves;  // wave-uniform
+    const int wb = builder ? w : 0;
+    char *const region = lds + wb * kRegion;
     float *const stage = reinterpret_cast<float *>(region);
     u32x4_t *const frags = reinterpret_cast<u32x4_t *>(region);
     const int kr = blockIdx.x;
@@ -624,7 +632,7 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     }
     const int K2 = (int)(a.K * 2);
     const int64_t kg0 = (int64_t)kr * kKs;            // first k-step of the workgroup
-    const int64_t ks0 = kg0 + (int64_t)w * kSmallKs;  // first k-step this wave builds
+    const int64_t ks0 = kg0 + (int64_t)wb * kSmallKs;  // first k-step this wave builds
 
     // x as whole 128-byte lines (two k-steps of a row): for pair p, register
     // (i, p, h) holds, in lane l, row 16(w RBW + i) + 8h + (l & 7) and the 8
@@ -654,7 +662,9 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     f32x4_t phl[kPhiLoads];
     f32x4_t gm[kSmallKs][2];
     u32x4_t pf[kSmallKs][kPrep ? NT : 1];
-    if constexpr (kPrep) {
+    if (!builder) {
+        // No B to build: straight to the barrier.
+    } else if constexpr (kPrep) {
 #pragma unroll
         for (int kk = 0; kk < kSmallKs; ++kk) {
 #pragma unroll
@@ -679,7 +689,8 @@ __global__ __launch_bounds__(kSmallWaves * 64) void rows_small_kernel(RowsSmallA
     // Every load is issued before any use: one memory round trip.
     __builtin_amdgcn_sched_barrier(0);
 
-    if constexpr (kPrep) {
+    if (!builder) {
+    } else if constexpr (kPrep) {
 #pragma unroll
         for (int kk = 0; kk < kSmallKs; ++kk) {
 #pragma unroll
@@ -1086,10 +1097,10 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
         sa.K = p.K;
         if (bprep != nullptr) {
             hipLaunchKernelGGL((rows_small_kernel<N, kBf16, true>), dim3((unsigned)p.rowsS),
-                               dim3(kSmallWaves * 64), 0, stream, sa);
+                               dim3(small_waves<N>() * 64), 0, stream, sa);
         } else {
             hipLaunchKernelGGL((rows_small_kernel<N, kBf16, false>), dim3((unsigned)p.rowsS),
-                               dim3(kSmallWaves * 64), 0, stream, sa);
+                               dim3(small_waves<N>() * 64), 0, stream, sa);
         }
     } else {
         // Without prepared weights the GEMM builds each stage's B from phi
