@@ -353,9 +353,18 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
         // Small batches: one K-range per workgroup of the small-batch GEMM,
         // which builds B from phi itself (each element of B is used once).
+        // Its wide variant (twice the rows and waves) takes the next band of
+        // T when the rows are long: measured on MI355X (back to back, us,
+        // small-batch / block GEMM): n = 4, D = 7168, T = 160 11.8 / 12.6,
+        // T = 256 13.1 / 14.6; D = 4096, T = 256 12.3 / 13.6; n = 8, D = 7168,
+        // T = 128 19.9 / 22.4; D = 2048 (K = 16384), T = 128 13.8 / 14.4;
+        // n = 6, D = 4096, T = 128 12.7 / 14.0; but D = 1024, T = 256 10.9 /
+        // 10.2 and fp16 D = 2048, T = 256 13.4 / 11.4 (K < 16384).  Its x
+        // offsets (every row it holds, past T too) stay below 2^31.
         const int64_t smallKs = mhc::rows_small_ksteps();
-        if (T <= mhc::rows_small_rows(n) && ((K / 32) % smallKs) == 0 &&
-            T * K * 2 < (int64_t{1} << 31)) {
+        const bool wide = T > mhc::rows_small_rows(n, false);
+        if (T <= mhc::rows_small_rows(n, wide) && (!wide || K >= 16384) && ((K / 32) % smallKs) == 0 &&
+            mhc::rows_small_rows(n, wide) * K * 2 < (int64_t{1} << 31)) {
             p.rowsSmall = true;
             p.rowsS = static_cast<int>((K / 32) / smallKs);
         }
@@ -388,10 +397,12 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         // bf16 with gamma unless noted, rows / strip): T <= 128 rows at every
         // width (D = 7168: T = 64 10.4 / 12.2, T = 128 11.8 / 12.4; fp16
         // without gamma T = 96 11.9 / 12.6, T = 128 12.9 / 12.6, the one
-        // loss); T = 160 rows up to D = 6144 (13.0 / 13.2; D = 7168 13.7 /
-        // 13.5); up to T = 256 rows while T * D <= 2^19 (D = 2048, T = 256
-        // 11.6 / 12.3; D = 3072, T = 192 12.1 / 12.3 and D = 4096, T = 192
-        // 13.3 / 12.9 stay strip); up to T = 1024 while T * D <= 3 * 2^17
+        // loss); T = 160 rows up to D = 6144 (13.0 / 13.2); up to T = 256
+        // rows from D = 4096, on the wide small-batch GEMM (D = 7168, T =
+        // 160 11.8 / 13.6, T = 256 13.1 / 13.9; D = 4096, T = 192 11.4 /
+        // 12.7, T = 256 12.3 / 13.0) and below while T * D <= 2^19 (D =
+        // 2048, T = 256 11.6 / 12.3; D = 3072, T = 192 12.1 / 12.3 stays
+        // strip); up to T = 1024 while T * D <= 3 * 2^17
         // (D = 768, T = 512 11.5 / 11.7; D = 256, T = 1024 10.8 / 11.9;
         // D = 512, T = 1024 12.4 / 11.7 and D = 1024, T = 512 12.5 / 12.3
         // stay strip).
@@ -409,7 +420,8 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         if (p.stripP > 0) {
             p.path = mhc::Path::kStrip;
             const int64_t td = T * D;
-            if (p.rowsS > 0 && (T <= 128 || (T <= 160 && D <= 6144) || (T <= 256 && td <= (int64_t{1} << 19)) ||
+            if (p.rowsS > 0 && (T <= 128 || (T <= 160 && D <= 6144) ||
+                                (T <= 256 && (p.rowsSmall || td <= (int64_t{1} << 19))) ||
                                 (T <= 1024 && td <= 3 * (int64_t{1} << 17)))) {
                 p.path = mhc::Path::kRows;
             }

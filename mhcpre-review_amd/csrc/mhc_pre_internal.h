@@ -95,8 +95,9 @@ struct Plan {
     // The block GEMM builds B from phi and gamma itself (no prep launch);
     // otherwise a prep kernel writes B fragments to the workspace first.
     bool rowsBFromPhi = false;
-    // Small batches (T <= rows_small_rows(n)): one GEMM workgroup per K-range
-    // of rows_small_ksteps() k-steps, B built from phi in registers, no prep.
+    // Small batches (T <= rows_small_rows(n, false), or up to twice that with
+    // K >= 16384): one GEMM workgroup per K-range of rows_small_ksteps()
+    // k-steps, B built from phi by the workgroup itself, no prep launch.
     bool rowsSmall = false;
     // Partial sums stored row-major, [T][rowsS][M+1] (each row's sums
     // contiguous for its epilogue), instead of [rowsS][T][M+1].
@@ -168,7 +169,8 @@ int rows_block_rows();
 int rows_stage_ksteps();
 int rows_gemm_threads();
 // Largest batch of the small-batch GEMM and k-steps per workgroup there.
-int rows_small_rows(int n);
+// Rows the small-batch GEMM holds (the wide variant: twice as many).
+int rows_small_rows(int n, bool wide);
 int rows_small_ksteps();
 
 // Stream probe (mhc_pre_stream.hip): reads readBytes (a multiple of 4096) from

@@ -72,15 +72,16 @@ constexpr int kStageKs = 2;                  // k-steps per stage (kStageKs / 2 
 constexpr int kAhead = 3;                    // stages of x loading ahead of the MFMAs
 constexpr int kXSlots = kAhead + 1;          // x register ring
 constexpr int kBSets = kAhead - 1;           // B staging register sets
-// Small-batch GEMM: rows held by every wave (n = 4 has 2 accumulator tiles
-// per 16 rows, n = 6 and 8 have 3 and 5).
+// Small-batch GEMM: rows of a workgroup (n = 4 has 2 accumulator tiles per
+// 16 rows, n = 6 and 8 have 3 and 5); the wide variant holds twice as many.
 template <int N>
 constexpr int small_rows() { return N == 4 ? 128 : 64; }
 constexpr int kSmallWaves = 4;               // small-batch GEMM: waves building a K-range's B
 // Small-batch GEMM: waves per workgroup, each multiplying its own 16-row
-// blocks (n = 4: 8 waves of one block; n = 6, 8: 4 waves of one block).
-template <int N>
-constexpr int small_waves() { return N == 4 ? 8 : 4; }
+// block (n = 4: 8 waves; n = 6, 8: 4 waves; twice as many in the wide
+// variant).
+template <int N, bool kWide>
+constexpr int small_waves() { return (N == 4 ? 8 : 4) * (kWide ? 2 : 1); }
 constexpr int kSmallKs = 2;                  // small-batch GEMM: k-steps per wave
 
 // Column tiles of the B operand and the accumulator tile each one adds into.
@@ -593,8 +594,8 @@ struct RowsSmallArgs {
     int64_t K;
 };
 
-template <int N, bool kBf16, bool kPrep>
-__global__ __launch_bounds__(small_waves<N>() * 64) void rows_small_kernel(RowsSmallArgs a)
+template <int N, bool kBf16, bool kPrep, bool kWide>
+__global__ __launch_bounds__((small_waves<N, kWide>() * 64)) void rows_small_kernel(RowsSmallArgs a)
 {
     using C = RowsCols<N>;
     constexpr int M = C::M;
@@ -602,10 +603,10 @@ __global__ __launch_bounds__(small_waves<N>() * 64) void rows_small_kernel(RowsS
     constexpr int NT = C::NT;
     constexpr int Q = C::Q;
     constexpr int kKs = kSmallWaves * kSmallKs;          // k-steps per workgroup
-    constexpr int RBW = small_rows<N>() / 16 / small_waves<N>();  // row blocks per wave
+    constexpr int RBW = small_rows<N>() * (kWide ? 2 : 1) / 16 / small_waves<N, kWide>();  // row blocks per wave
     static_assert(kSmallKs == 2, "one 128-byte line of each row per k-step pair");
     static_assert(RBW >= 1, "every wave holds at least one row block");
-    static_assert(small_waves<N>() >= kSmallWaves, "every builder wave also multiplies");
+    static_assert(small_waves<N, kWide>() >= kSmallWaves, "every builder wave also multiplies");
     // LDS: one region per builder wave.  It first holds the wave's phi block in row
     // order (row pitch kPhiPitch floats: consecutive rows start 4 banks
     // apart), which the wave reads back in B-fragment order, then the
@@ -1095,12 +1096,22 @@ hipError_t launch_rows_t(const Plan &p, void *workspace, int nXcd, hipStream_t s
         sa.status = status;
         sa.T = p.T;
         sa.K = p.K;
-        if (bprep != nullptr) {
-            hipLaunchKernelGGL((rows_small_kernel<N, kBf16, true>), dim3((unsigned)p.rowsS),
-                               dim3(small_waves<N>() * 64), 0, stream, sa);
+        // More rows than the narrow variant holds: the wide one.
+        const dim3 grid((unsigned)p.rowsS);
+        if (p.T > small_rows<N>()) {
+            const dim3 block(small_waves<N, true>() * 64);
+            if (bprep != nullptr) {
+                hipLaunchKernelGGL((rows_small_kernel<N, kBf16, true, true>), grid, block, 0, stream, sa);
+            } else {
+                hipLaunchKernelGGL((rows_small_kernel<N, kBf16, false, true>), grid, block, 0, stream, sa);
+            }
         } else {
-            hipLaunchKernelGGL((rows_small_kernel<N, kBf16, false>), dim3((unsigned)p.rowsS),
-                               dim3(small_waves<N>() * 64), 0, stream, sa);
+            const dim3 block(small_waves<N, false>() * 64);
+            if (bprep != nullptr) {
+                hipLaunchKernelGGL((rows_small_kernel<N, kBf16, true, false>), grid, block, 0, stream, sa);
+            } else {
+                hipLaunchKernelGGL((rows_small_kernel<N, kBf16, false, false>), grid, block, 0, stream, sa);
+            }
         }
     } else {
         // Without prepared weights the GEMM builds each stage's B from phi
@@ -1244,7 +1255,10 @@ bool rows_epilogue_wide(int n, int S, int64_t rows)
 
 int rows_block_rows() { return kRowBlock; }
 int rows_gemm_threads() { return kRW * 64; }
-int rows_small_rows(int n) { return n == 4 ? small_rows<4>() : n == 6 ? small_rows<6>() : small_rows<8>(); }
+int rows_small_rows(int n, bool wide)
+{
+    return (n == 4 ? small_rows<4>() : n == 6 ? small_rows<6>() : small_rows<8>()) * (wide ? 2 : 1);
+}
 int rows_small_ksteps() { return kSmallWaves * kSmallKs; }
 int rows_stage_ksteps() { return kStageKs; }
 

@@ -339,6 +339,10 @@ def test_shared_workspace_back_to_back(pkg, orc, device, force, expect, n, T, D)
     (24, 8, 3088, True, True),      # 3 parts of 129 / 129 / 128 octets
     (100, 4, 256, False, False),    # n = 4 small-batch GEMM (128 rows per wave), 100 rows
     (128, 4, 7168, True, True),     # n = 4 small-batch GEMM, full 128 rows, K = 28672
+    (200, 4, 4096, True, True),     # wide small-batch GEMM (n = 4: 256 rows), 200 rows
+    (256, 4, 7168, False, True),    # wide small-batch GEMM, full 256 rows, fp16
+    (128, 6, 4096, True, False),    # wide small-batch GEMM (n = 6, 8: 128 rows), full
+    (65, 8, 2048, True, True),      # wide small-batch GEMM, one row past the narrow one
 ])
 def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     """Row-block path (n = 6, 8): ragged row blocks, several K-ranges, fp16 and

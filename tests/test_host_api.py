@@ -248,9 +248,11 @@ def _path(pkg, lib, d, env=None):
     (4, 5632, 1, "rows"),
     (4, 4096, 160, "rows"),    # T <= 160 up to D = 6144
     (4, 6144, 160, "rows"),
-    (4, 7168, 129, "strip"),
-    (4, 7168, 160, "strip"),
-    (4, 4096, 161, "strip"),   # T <= 256: rows while T * D <= 2^19
+    (4, 7168, 129, "rows"),    # T <= 256 from D = 4096: the wide small-batch GEMM
+    (4, 7168, 256, "rows"),
+    (4, 4096, 256, "rows"),
+    (4, 7168, 257, "strip"),
+    (4, 3584, 161, "strip"),   # T <= 256 below D = 4096: rows while T * D <= 2^19
     (4, 2048, 256, "rows"),
     (4, 3072, 192, "strip"),
     (4, 2048, 257, "strip"),   # T <= 1024: rows while T * D <= 3 * 2^17

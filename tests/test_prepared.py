@@ -174,6 +174,8 @@ def _check_oracle(orc, host, outs, bf16):
     (300, 6, 2048, False, True, None, "rows"),
     (40, 8, 4096, True, True, None, "rows"),      # small-batch GEMM
     (100, 4, 256, False, False, None, "rows"),    # n = 4 small batch
+    (200, 4, 4096, True, True, None, "rows"),     # n = 4 wide small batch
+    (100, 8, 2048, False, True, None, "rows"),    # n = 8 wide small batch
 ])
 def test_prepared_matches_plain(pkg, orc, device, T, n, D, bf16, gamma_on, force, path):
     import torch
@@ -228,6 +230,7 @@ def test_rows_gemm_b_sources_match(pkg, orc, device, T, n, D, bf16, gamma_on, fo
     (40, 8, 4096, True, True, None),        # small-batch GEMM, rows past T in the last block
     (64, 8, 7168, False, False, None),      # 224 K-ranges: the 1024-thread epilogue in 4 parts
     (64, 6, 1024, True, True, None),
+    (200, 4, 4096, False, True, None),      # wide small-batch GEMM
     (300, 4, 512, True, True, None),        # block GEMM, B built from phi, the half tile
     (600, 8, 1024, True, True, "rows"),
     (4200, 8, 512, False, False, "rows"),   # 17 row blocks: the prep launch
