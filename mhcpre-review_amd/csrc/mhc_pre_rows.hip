@@ -77,11 +77,16 @@ constexpr int kBSets = kAhead - 1;           // B staging register sets
 template <int N>
 constexpr int small_rows() { return N == 4 ? 128 : 64; }
 constexpr int kSmallWaves = 4;               // small-batch GEMM: waves building a K-range's B
-// Small-batch GEMM: waves per workgroup, each multiplying its own 16-row
-// block (n = 4: 8 waves; n = 6, 8: 4 waves; twice as many in the wide
-// variant).
+// Small-batch GEMM: waves per workgroup.  Each multiplies one 16-row block
+// by a share of the K-range: half of it in the narrow n = 6 and 8 variants
+// (two waves per block), all of it otherwise.  Measured on MI355X (back to
+// back, us, one wave / two waves per block): n = 8, D = 7168, T = 64 16.1 /
+// 15.5; n = 8, D = 4096, T = 64 14.2 / 13.7; n = 4, D = 7168, T = 128
+// 10.5 / 10.9 (16 waves of 89 VGPRs).
 template <int N, bool kWide>
-constexpr int small_waves() { return (N == 4 ? 8 : 4) * (kWide ? 2 : 1); }
+constexpr int small_split() { return (kWide || N == 4) ? 1 : 2; }
+template <int N, bool kWide>
+constexpr int small_waves() { return small_rows<N>() * (kWide ? 2 : 1) / 16 * small_split<N, kWide>(); }
 constexpr int kSmallKs = 2;                  // small-batch GEMM: k-steps per wave
 
 // Column tiles of the B operand and the accumulator tile each one adds into.
@@ -572,14 +577,16 @@ __global__ __launch_bounds__(kRW * 64) void rows_gemm_kernel(RowsGemmArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// rows_small: decode-shaped batches (T <= small_rows(n)).  One workgroup per
-// K-range of kSmallWaves * kSmallKs k-steps.  Each of the first kSmallWaves
-// waves builds the B fragments of kSmallKs of them from phi and gamma (or
-// copies them from the prepared buffer) into LDS; after one barrier every
-// wave multiplies its own 16-row blocks by all of the K-range's fragments
-// and writes its rows' partial sums from registers.  Rows past T read as
-// zeros and are not written; a wave whose blocks all start at or past T
-// skips the products.
+// rows_small: decode-shaped batches (T <= small_rows(n), or twice that in
+// the wide variant).  One workgroup per K-range of kSmallWaves * kSmallKs
+// k-steps.  Each of the first kSmallWaves waves builds the B fragments of
+// kSmallKs of them from phi and gamma (or copies them from the prepared
+// buffer) into LDS; after one barrier every wave multiplies its 16-row block
+// by its share of the K-range's fragments (the first or second half in the
+// narrow n = 6 and 8 variants, whose two sums per block then meet in LDS in
+// that order; all of them otherwise) and the block's partial sums go out
+// from registers.  Rows past T read as zeros and are not written; a block that
+// starts at or past T skips the products.
 // ---------------------------------------------------------------------------
 struct RowsSmallArgs {
     const uint16_t *x;
@@ -603,9 +610,11 @@ __global__ __launch_bounds__((small_waves<N, kWide>() * 64)) void rows_small_ker
     constexpr int NT = C::NT;
     constexpr int Q = C::Q;
     constexpr int kKs = kSmallWaves * kSmallKs;          // k-steps per workgroup
-    constexpr int RBW = small_rows<N>() * (kWide ? 2 : 1) / 16 / small_waves<N, kWide>();  // row blocks per wave
+    constexpr int kBlocks = small_rows<N>() * (kWide ? 2 : 1) / 16;  // 16-row blocks
+    constexpr int kSplit = small_split<N, kWide>();      // waves per block
+    constexpr int kKsW = kKs / kSplit;                   // k-steps per wave
     static_assert(kSmallKs == 2, "one 128-byte line of each row per k-step pair");
-    static_assert(RBW >= 1, "every wave holds at least one row block");
+    static_assert(kKsW % 2 == 0, "whole k-step pairs per wave");
     static_assert(small_waves<N, kWide>() >= kSmallWaves, "every builder wave also multiplies");
     // LDS: one region per builder wave.  It first holds the wave's phi block in row
     // order (row pitch kPhiPitch floats: consecutive rows start 4 banks
@@ -618,6 +627,10 @@ __global__ __launch_bounds__((small_waves<N, kWide>() * 64)) void rows_small_ker
     constexpr int kFragBytes = kSmallKs * NT * kWave * 16;
     constexpr int kRegion = kStageBytes > kFragBytes ? kStageBytes : kFragBytes;
     __shared__ __attribute__((aligned(16))) char lds[kSmallWaves * kRegion];
+    // After the products the second-half waves' sums pass through the same
+    // LDS: [block][NA accumulator tiles + Gram tile][64 lanes].
+    static_assert(kSplit == 1 || kBlocks * (NA + 1) * kWave * 16 <= kSmallWaves * kRegion,
+                  "the half sums fit the fragment regions");
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -634,25 +647,24 @@ __global__ __launch_bounds__((small_waves<N, kWide>() * 64)) void rows_small_ker
     const int K2 = (int)(a.K * 2);
     const int64_t kg0 = (int64_t)kr * kKs;            // first k-step of the workgroup
     const int64_t ks0 = kg0 + (int64_t)wb * kSmallKs;  // first k-step this wave builds
+    const int rb = w % kBlocks;                        // this wave's 16-row block
+    const int half = w / kBlocks;                      // its share of the k-steps
+    const int kw0 = half * kKsW;                       // first k-step (in the range) it multiplies
 
     // x as whole 128-byte lines (two k-steps of a row): for pair p, register
-    // (i, p, h) holds, in lane l, row 16(w RBW + i) + 8h + (l & 7) and the 8
-    // k at 8(l >> 4) + 32((l >> 3) & 1) of k-steps kg0 + 2p and kg0 + 2p + 1;
+    // (p, h) holds, in lane l, row 16 rb + 8h + (l & 7) and the 8 k at
+    // 8(l >> 4) + 32((l >> 3) & 1) of k-steps kg0 + kw0 + 2p and the next;
     // a DPP exchange turns each pair into the A fragments of the two.
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, T * K2);
-    constexpr int kPairs = kKs / 2;
-    u32x4_t xln[RBW][kPairs][2];
+    constexpr int kPairs = kKsW / 2;
+    u32x4_t xln[kPairs][2];
 #pragma unroll
-    for (int i = 0; i < RBW; ++i) {
-        const int rowBase = 16 * (w * RBW + i);
+    for (int p = 0; p < kPairs; ++p) {
 #pragma unroll
-        for (int p = 0; p < kPairs; ++p) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                xln[i][p][h] = load16<kCpolNt>(xr, (rowBase + 8 * h + (lane & 7)) * K2 +
-                                                       (int)((kg0 + 2 * p) * 64) + 16 * (lane >> 4) +
-                                                       64 * ((lane >> 3) & 1));
-            }
+        for (int h = 0; h < 2; ++h) {
+            xln[p][h] = load16<kCpolNt>(xr, (16 * rb + 8 * h + (lane & 7)) * K2 +
+                                                (int)((kg0 + kw0 + 2 * p) * 64) + 16 * (lane >> 4) +
+                                                64 * ((lane >> 3) & 1));
         }
     }
     // phi rows as whole 256-byte runs (the wave's 64 k of 4 rows per load),
@@ -760,109 +772,116 @@ __global__ __launch_bounds__((small_waves<N, kWide>() * 64)) void rows_small_ker
     }
     lds_barrier();
 
-    // Row blocks of this wave that hold rows below T (wave-uniform).
-    const int live = min(RBW, max(0, (T - 16 * w * RBW + 15) / 16));
-    if (live == 0) {
-        return;
-    }
-    u32x4_t xa[kKs][RBW];
+    // Whether this wave's block holds rows below T (wave-uniform).
+    const bool live = 16 * rb < T;
+    f32x4_t acc[NA];
+    f32x4_t gram = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < RBW; ++i) {
+    for (int t = 0; t < NA; ++t) {
+        acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    if (live) {
+        u32x4_t xa[kKsW];
 #pragma unroll
         for (int p = 0; p < kPairs; ++p) {
-            lines_to_frags(xln[i][p][0], xln[i][p][1], xa[2 * p][i], xa[2 * p + 1][i]);
+            lines_to_frags(xln[p][0], xln[p][1], xa[2 * p], xa[2 * p + 1]);
         }
-    }
-    f32x4_t acc[RBW][NA];
-    f32x4_t gram[RBW];
+        // This wave's k-steps in order: k-step kk's fragments were built by
+        // wave kk / kSmallKs.
 #pragma unroll
-    for (int i = 0; i < RBW; ++i) {
-        gram[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < kKsW; ++q) {
+            const int kk = kw0 + q;
+            const u32x4_t *src = reinterpret_cast<const u32x4_t *>(lds + (kk / kSmallKs) * kRegion) +
+                                 (kk % kSmallKs) * NT * kWave + lane;
+            u32x4_t bf[NT];
 #pragma unroll
-        for (int t = 0; t < NA; ++t) {
-            acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    // k-steps in order: k-step kk's fragments were built by wave kk / kSmallKs.
-#pragma unroll
-    for (int kk = 0; kk < kKs; ++kk) {
-        const u32x4_t *src = reinterpret_cast<const u32x4_t *>(lds + (kk / kSmallKs) * kRegion) +
-                             (kk % kSmallKs) * NT * kWave + lane;
-        u32x4_t bf[NT];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            bf[t] = src[t * kWave];
-        }
-#pragma unroll
-        for (int i = 0; i < RBW; ++i) {
-            if (i >= live) {
-                continue;
+            for (int t = 0; t < NT; ++t) {
+                bf[t] = src[t * kWave];
             }
             u32x4_t xh, xl;
             if constexpr (!kBf16) {
                 float fx[8];
-                unpack8<false>(xa[kk][i], fx);
+                unpack8<false>(xa[q], fx);
                 split_f16_to_bf16(fx, xh, xl);
             }
 #pragma unroll
             for (int t = 0; t < Q; ++t) {
                 if constexpr (kBf16) {
-                    acc[i][t] = mfma16(xa[kk][i], bf[t], acc[i][t]);
-                    acc[i][t] = mfma16(xa[kk][i], bf[Q + t], acc[i][t]);
+                    acc[t] = mfma16(xa[q], bf[t], acc[t]);
+                    acc[t] = mfma16(xa[q], bf[Q + t], acc[t]);
                 } else {
-                    acc[i][t] = mfma16(xh, bf[t], acc[i][t]);
-                    acc[i][t] = mfma16(xh, bf[Q + t], acc[i][t]);
-                    acc[i][t] = mfma16(xl, bf[t], acc[i][t]);
+                    acc[t] = mfma16(xh, bf[t], acc[t]);
+                    acc[t] = mfma16(xh, bf[Q + t], acc[t]);
+                    acc[t] = mfma16(xl, bf[t], acc[t]);
                 }
             }
             if constexpr (C::kHalf) {
                 if constexpr (kBf16) {
-                    acc[i][Q] = mfma16(xa[kk][i], bf[2 * Q], acc[i][Q]);
+                    acc[Q] = mfma16(xa[q], bf[2 * Q], acc[Q]);
                 } else {
-                    acc[i][Q] = mfma16(xh, bf[2 * Q], acc[i][Q]);
-                    acc[i][Q] = mfma16(xl, bf[2 * Q], acc[i][Q]);
+                    acc[Q] = mfma16(xh, bf[2 * Q], acc[Q]);
+                    acc[Q] = mfma16(xl, bf[2 * Q], acc[Q]);
                 }
             }
             if constexpr (kBf16) {
-                gram[i] = mfma16(xa[kk][i], xa[kk][i], gram[i]);
+                gram = mfma16(xa[q], xa[q], gram);
             } else {
-                gram[i] = mfma16_f16(xa[kk][i], xa[kk][i], gram[i]);
+                gram = mfma16_f16(xa[q], xa[q], gram);
             }
         }
     }
+    if constexpr (kSplit == 2) {
+        // The second half's sums, added to the first half's in that order.
+        // Every wave takes both barriers (the first: all fragment reads are
+        // done before the regions are overwritten).
+        f32x4_t *red = reinterpret_cast<f32x4_t *>(lds) + rb * (NA + 1) * kWave + lane;
+        lds_barrier();
+        if (half == 1 && live) {
+#pragma unroll
+            for (int t = 0; t < NA; ++t) {
+                red[t * kWave] = acc[t];
+            }
+            red[NA * kWave] = gram;
+        }
+        lds_barrier();
+        if (half == 1 || !live) {
+            return;
+        }
+#pragma unroll
+        for (int t = 0; t < NA; ++t) {
+            acc[t] = acc[t] + red[t * kWave];
+        }
+        gram = gram + red[NA * kWave];
+    } else if (!live) {
+        return;
+    }
 
-    // Partial sums of this wave's rows (C fragment: lane l, register e holds
-    // row 4(l >> 4) + e, column l & 15 of its tile); read once, by the
+    // Partial sums of this block's rows (C fragment: lane l, register e
+    // holds row 4(l >> 4) + e, column l & 15 of its tile); read once, by the
     // epilogue.
     float *dst = a.partial + (int64_t)kr * a.rangeStride;
 #pragma unroll
-    for (int i = 0; i < RBW; ++i) {
-        if (i >= live) {
-            continue;
+    for (int e = 0; e < 4; ++e) {
+        const int row = 16 * rb + 4 * (lane >> 4) + e;
+        const bool ok = row < T;
+        float *drow = dst + (int64_t)row * a.rowStride;
+#pragma unroll
+        for (int t = 0; t < Q; ++t) {
+            if (ok) {
+                __builtin_nontemporal_store(acc[t][e], &drow[16 * t + (lane & 15)]);
+            }
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int row = 16 * (w * RBW + i) + 4 * (lane >> 4) + e;
-            const bool ok = row < T;
-            float *drow = dst + (int64_t)row * a.rowStride;
-#pragma unroll
-            for (int t = 0; t < Q; ++t) {
-                if (ok) {
-                    __builtin_nontemporal_store(acc[i][t][e], &drow[16 * t + (lane & 15)]);
-                }
+        if constexpr (C::kHalf) {
+            // hi in lanes 0-7 of each 16, lo of the same column 8 lanes up.
+            const float v = acc[Q][e];
+            const float lo = row_swap8(v);
+            if (ok && (lane & 15) < 8) {
+                __builtin_nontemporal_store(v + lo, &drow[16 * Q + (lane & 7)]);
             }
-            if constexpr (C::kHalf) {
-                // hi in lanes 0-7 of each 16, lo of the same column 8 lanes up.
-                const float v = acc[i][Q][e];
-                const float lo = row_swap8(v);
-                if (ok && (lane & 15) < 8) {
-                    __builtin_nontemporal_store(v + lo, &drow[16 * Q + (lane & 7)]);
-                }
-            }
-            // Diagonal of the Gram tile: the row's sum of squares.
-            if (ok && (lane & 15) == 4 * (lane >> 4) + e) {
-                __builtin_nontemporal_store(gram[i][e], &drow[M]);
-            }
+        }
+        // Diagonal of the Gram tile: the row's sum of squares.
+        if (ok && (lane & 15) == 4 * (lane >> 4) + e) {
+            __builtin_nontemporal_store(gram[e], &drow[M]);
         }
     }
 }
