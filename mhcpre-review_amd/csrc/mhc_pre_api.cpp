@@ -435,16 +435,20 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
     } else {
         p.path = p.rowsS > 0 ? mhc::Path::kRows : mhc::Path::kSplit;
-        // Short rows (K <= 12288) and one to two thousand rows: the rows path
-        // has few row blocks to spread (256 rows each) and many partial sums
-        // per row to add, and the split path's 16-row tiles are faster.
-        // Measured on MI355X, back to back (rows / split, us): n = 6, D =
-        // 1024: T = 256 12.8 / 14.6, 512 15.2 / 16.0, 1024 23.2 / 18.9, 2048
-        // 35.2 / 25.9; n = 6, D = 2048: T = 512 20.5 / 22.6, 1024 30.5 /
-        // 28.9, 2048 41.6 / 40.2; n = 8, D = 1024: T = 256 15.7 / 19.0, 512
-        // 22.4 / 20.6, 1024 31.8 / 28.1, 2048 40.6 / 40.2; n = 8, D = 512,
-        // T = 1024 25.3 / 17.6; n = 8, D = 2048 (K = 16384) rows at every T.
-        if (p.path == mhc::Path::kRows && !p.rowsSmall && K <= 12288 && T <= 2048 &&
+        // Short rows (K <= 9216) from a thousand rows: the rows path reads x
+        // twice and adds many partial sums per row, while the split path's
+        // 16-row tiles stream x once per kernel with few partials.  Measured
+        // on MI355X, back to back (rows / split, us): n = 6, D = 512: T =
+        // 2048 28.4 / 17.1, 4096 43.7 / 26.2, 8192 64.7 / 39.2; n = 6, D =
+        // 1024: T = 512 14.8 / 16.2, 1024 22.2 / 18.8, 4096 49.4 / 39.7, 8192
+        // 76.7 / 62.0; n = 6, D = 1536: T = 1024 24.3 / 24.6, 2048 37.2 /
+        // 33.4, 8192 89.5 / 86.3; n = 8, D = 512: T = 1024 24.4 / 17.9, 8192
+        // 80.4 / 58.8; n = 8, D = 1024: T = 512 21.8 / 21.0, 1024 31.7 /
+        // 28.4, 4096 63.6 / 60.4, 8192 101.9 / 99.1.  From K = 12288 the rows
+        // path is as fast or faster (n = 6, D = 2048: T = 1024 28.7 / 29.1,
+        // 2048 40.9 / 40.3, 8192 108.9 / 110.9; n = 8, D = 1536: T = 1024
+        // 32.5 / 35.9, 2048 46.5 / 51.3, 8192 126.1 / 142.7).
+        if (p.path == mhc::Path::kRows && !p.rowsSmall && K <= 9216 &&
             (T >= 1024 || (T >= 512 && n == 8 && K <= 8192))) {
             p.path = mhc::Path::kSplit;
         }

@@ -364,8 +364,8 @@ def test_rows_path_shapes(pkg, orc, device, T, n, D, is_bf16, has_gamma):
     check(out, ref, x, is_bf16, orc)
 
 
-@pytest.mark.parametrize("n,want", [(4, "split"), (8, "rows")])
-def test_epilogue_launches_in_row_chunks(pkg, orc, device, n, want):
+@pytest.mark.parametrize("n,force,want", [(4, None, "split"), (8, None, "split"), (8, "rows", "rows")])
+def test_epilogue_launches_in_row_chunks(pkg, orc, device, n, force, want):
     """More than 2^20 rows: the one-workgroup-per-row epilogues run as several
     launches (a grid's work-items must stay below 2^32).  The rows on both
     sides of the launch boundary and the last rows are checked against the
@@ -379,8 +379,8 @@ def test_epilogue_launches_in_row_chunks(pkg, orc, device, n, want):
     alpha = np.asarray([0.3, -0.2, 0.05], dtype=np.float32)
     bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
     gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
-    _say(f"[chunks] T={T} n={n} D={D}")
-    out = run_gpu(pkg, device, x, True, phi, alpha, bias, gamma)
+    _say(f"[chunks] T={T} n={n} D={D} force={force}")
+    out = run_gpu(pkg, device, x, True, phi, alpha, bias, gamma, force_path=force)
     assert out["path"] == want
     sel = np.r_[0:4, (1 << 20) - 8:(1 << 20) + 8, T - 8:T]
     ref = orc.mhc_pre(x[sel], True, phi, alpha, bias, gamma)

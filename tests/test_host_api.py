@@ -265,18 +265,22 @@ def _path(pkg, lib, d, env=None):
     (8, 7168, 64, "rows"),     # n = 8, K % 128 == 0
     (8, 8192, 5472, "rows"),
     (6, 1024, 16, "rows"),     # K = 6144
-    (6, 1024, 2048, "split"),  # K <= 12288, 1024 <= T <= 2048
+    (6, 1024, 2048, "split"),  # K <= 9216 from T = 1024
     (6, 1024, 1024, "split"),
+    (6, 1024, 8192, "split"),
+    (6, 512, 4096, "split"),
+    (6, 1536, 1024, "split"),  # K = 9216
     (6, 1024, 512, "rows"),
     (8, 1024, 1024, "split"),
+    (8, 1024, 4096, "split"),
     (8, 1024, 512, "split"),   # n = 8, K <= 8192: from T = 512
     (8, 1024, 511, "rows"),
     (8, 1024, 256, "rows"),
-    (8, 1024, 2049, "rows"),
-    (6, 2048, 512, "rows"),    # K = 12288: from T = 1024
-    (6, 2048, 1024, "split"),
-    (6, 2048, 2048, "split"),
-    (8, 1536, 1024, "split"),
+    (8, 1024, 2049, "split"),
+    (6, 2048, 512, "rows"),    # K = 12288: rows at every T
+    (6, 2048, 1024, "rows"),
+    (6, 2048, 8192, "rows"),
+    (8, 1536, 1024, "rows"),
     (8, 1536, 512, "rows"),
     (8, 2048, 1024, "rows"),   # K = 16384
     (6, 48, 16, "split"),      # K = 288: not a multiple of 128
