@@ -419,6 +419,13 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         // rows path cannot hold.
         if (p.stripP > 0) {
             p.path = mhc::Path::kStrip;
+            // One slice per team (D = 256) from T = 4096: the split path
+            // streams faster (strip / split, us: T = 4096 14.5 / 13.8, 8192
+            // 21.5 / 20.2, 32768 55.9 / 49.8; D = 512, T = 8192 22.8 / 28.3
+            // stays strip).
+            if (D == 256 && T >= 4096) {
+                p.path = mhc::Path::kSplit;
+            }
             const int64_t td = T * D;
             if (p.rowsS > 0 && (T <= 128 || (T <= 160 && D <= 6144) ||
                                 (T <= 256 && (p.rowsSmall || td <= (int64_t{1} << 19))) ||

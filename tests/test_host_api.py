@@ -260,6 +260,9 @@ def _path(pkg, lib, d, env=None):
     (4, 1024, 512, "strip"),
     (4, 256, 1024, "rows"),
     (4, 256, 1025, "strip"),
+    (4, 256, 4095, "strip"),
+    (4, 256, 4096, "split"),   # one slice per team from T = 4096
+    (4, 512, 8192, "strip"),
     (4, 512, 1024, "strip"),
     (4, 5696, 64, "rows"),     # not a strip width: rows, not fused
     (8, 7168, 64, "rows"),     # n = 8, K % 128 == 0
