@@ -10,7 +10,10 @@ hIn (fp16 / bf16):
     difference between the device's and the oracle's hPre moves it further.
     Those elements must still lie within 1 ulp + sum_s |dhPre[s] * x[s]| +
     the fp32 rounding of both n-term sums (2 n 2^-24 sum_s |hPre[s] x[s]|),
-    and they must be rare (at most 1 in 10^3).  The GEMM's summation order is
+    and they must be rare: at most 1 in 10^3, or 8 elements in outputs of a
+    few rows (one row with a far-off hPre column moves a handful of its
+    cancelling elements, which the fraction alone would fail at T = 1 or 2).
+    The GEMM's summation order is
     hardware-defined in the reference (CANN Cube) and cannot be matched, so
     hPre agrees to fp32 rounding, not bit for bit.
 """
@@ -124,4 +127,5 @@ def assert_hin(got_bits, want_bits, x_bits, is_bf16: bool, got_pre, want_pre, or
                                  f"propagation; first at {i}: diff {diff[i]:.3e} "
                                  f"bound {bound[i]:.3e} ({int(d[i])} ulp)")
         frac = far.sum() / far.size
-        assert frac <= max_rare_fraction, f"hIn: {frac:.2e} of elements beyond 1 ulp"
+        assert far.sum() <= max(max_rare_fraction * far.size, 8), \
+            f"hIn: {int(far.sum())} elements ({frac:.2e}) beyond 1 ulp"

@@ -17,6 +17,8 @@ the case reports how many elements that was.
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -26,13 +28,16 @@ from test_gpu_parity import _say, run_gpu
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 64
-N_CASES_N4 = 24
+# MHCPRE_RANDOM_CASES / MHCPRE_RANDOM_SEED_BASE widen or shift the draw for
+# longer sweeps; the defaults are the committed cases.
+N_CASES = int(os.environ.get("MHCPRE_RANDOM_CASES", "64"))
+N_CASES_N4 = int(os.environ.get("MHCPRE_RANDOM_CASES_N4", "24"))
+SEED_BASE = int(os.environ.get("MHCPRE_RANDOM_SEED_BASE", "0"))
 MAX_ELEMS = 6_000_000  # T * n * D per case
 
 
 def random_case(i: int):
-    rng = np.random.default_rng(0x5EED0000 + i)
+    rng = np.random.default_rng(0x5EED0000 + SEED_BASE + i)
     n = int(rng.choice([4, 6, 8]))
     # Widths that reach every path: multiples of 256 (strip), of 64 (fused),
     # of 128 / n (rows), and of 16 only (split).
