@@ -97,7 +97,12 @@ typedef struct mhcPreExecutor mhcPreExecutor;
  *   hPost  fp32         [B, S, n]
  *   hRes   fp32         [B, S, n, n]
  * On success *workspaceSize holds the bytes the caller must allocate and
- * *executor a new executor (free it with mhcPreExecutorDestroy).
+ * *executor a new executor (free it with mhcPreExecutorDestroy).  The size is
+ * that of the launch path the plan takes.  On the strip path (n = 4, D a
+ * multiple of 256 up to 7936, all but small batches) it holds per-team
+ * exchange rings only and does not grow with T (7.2 MB at n = 4, D = 7168);
+ * the team count is that of the device holding x (of MI355X when the runtime
+ * cannot tell).  The two-pass paths hold partial sums that grow with T.
  */
 MHC_API int mhcPreGetWorkspaceSize(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alpha,
                            const mhcTensor *bias, const mhcTensor *gamma, float normEps,
@@ -124,7 +129,10 @@ MHC_API int mhcPreGetWorkspaceSizeWithHPre(const mhcTensor *x, const mhcTensor *
  * waiting.  The workspace must hold at least the bytes phase 1 returned.  The
  * device holding the tensors must be the current device
  * (MHC_STATUS_DEVICE_MISMATCH otherwise), as aclnn launches run on the
- * context's device.
+ * context's device.  A strip executor on a device that cannot co-schedule the
+ * teams phase 1 planned for (which MI355X always can) runs a fallback path only
+ * if the workspace holds that path's layout, and returns
+ * MHC_STATUS_UNSUPPORTED_SHAPE otherwise.
  *
  * The strip and fused kernels' workgroups wait on each other (bounded), so
  * their grids are sized to what the device holds at once.  By default it is a

@@ -95,12 +95,13 @@ struct DeviceShape {
     int xcds = 0;
 };
 
-bool device_shape(int &device, DeviceShape &out)
+// CUs and XCDs of `device` (cached per device).
+bool device_shape_of(int device, DeviceShape &out)
 {
     constexpr int kMaxDevices = 64;
     static std::mutex mu;
     static DeviceShape cache[kMaxDevices] = {};
-    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+    if (device < 0 || device >= kMaxDevices) {
         return false;
     }
     std::lock_guard<std::mutex> lock(mu);
@@ -123,6 +124,21 @@ bool device_shape(int &device, DeviceShape &out)
     out = cache[device];
     return true;
 }
+
+// The current device and its shape.
+bool device_shape(int &device, DeviceShape &out)
+{
+    if (hipGetDevice(&device) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return device_shape_of(device, out);
+}
+
+// MI355X: 256 CUs in 8 XCDs.  Phase 1 plans a strip executor's exchange rings
+// for the device that holds x, or for this shape when the runtime cannot
+// tell which device that is.
+constexpr DeviceShape kPlanShapeDefault{256, 8};
 
 // Device that holds the device memory at `p`, or -1 when the runtime cannot
 // tell (host memory, an address no allocation covers, no device visible).
@@ -482,9 +498,31 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
     }
 
-    // Workspace: header, then the split regions and the fused regions, which
-    // overlap (one launch at a time per workspace).  Sizes depend on the
-    // shape only, never on the device.
+    // Strip teams: those the device that holds x runs (MI355X's shape when
+    // the runtime cannot tell), at most one per row tile.  A device whose XCDs
+    // cannot hold one team takes the fused path (or the split path).
+    if (p.stripP > 0) {
+        DeviceShape shape = kPlanShapeDefault;
+        const int dev = device_of(p.x);
+        if (dev < 0 || !device_shape_of(dev, shape)) {
+            (void)hipGetLastError();
+            shape = kPlanShapeDefault;
+        }
+        const int teams = mhc::strip_teams_per_xcd(p.stripP, shape.cus / shape.xcds) * shape.xcds;
+        p.stripMaxTeams = static_cast<int>(std::min<int64_t>(rowTiles, teams));
+        if (teams < 1 && p.path == mhc::Path::kStrip) {
+            p.path = p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit;
+        }
+    }
+
+    // Workspace: the header, then the layout of the path the plan takes (a
+    // workspace holds one launch at a time).  The split layout holds B
+    // fragments and [S][T][M+1] partials; the fused layout a broadcast block
+    // and P records per row tile; the strip layout only per-team rings of
+    // them, so its size does not grow with T.  A fused plan also covers the
+    // split layout, its fallback on a device that cannot co-schedule a fused
+    // team; a strip executor runs a fallback only where its workspace holds
+    // that layout (phase 2 checks).
     const size_t splitBsplit = mhc::kWsHeaderBytes;
     const size_t splitPartial =
         align_up(splitBsplit + static_cast<size_t>(K) * static_cast<size_t>(2 * M) * 2, 256);
@@ -492,25 +530,20 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         align_up(splitPartial + static_cast<size_t>(S) * static_cast<size_t>(T) * (M + 1) * 4, 256);
     p.wsBsplit = splitBsplit;
     p.wsPartial = splitPartial;
-    // Fused and strip paths share the two exchange regions: per-tile blocks
-    // and records (fused), or per-team rings of them (strip), whichever is
-    // larger.
-    size_t fusedEnd = 0;
+    p.wsSplitEnd = splitEnd;
     if (p.fusedP > 0) {
-        size_t bcastSlots = static_cast<size_t>(rowTiles);
-        size_t recSlots = static_cast<size_t>(rowTiles);
-        if (p.stripP > 0) {
-            p.stripMaxTeams = static_cast<int>(
-                std::min<int64_t>(rowTiles, std::max(1, 1024 / (p.stripP + 1))));
-            const size_t ring = static_cast<size_t>(p.stripMaxTeams) * mhc::strip_ring_slots();
-            bcastSlots = std::max(bcastSlots, ring);
-            recSlots = std::max(recSlots, ring);
-        }
+        const size_t tiles = static_cast<size_t>(rowTiles);
         p.wsFinal = mhc::kWsHeaderBytes;
-        p.wsFusedPartial =
-            align_up(p.wsFinal + bcastSlots * mhc::fused_bcast_words(n) * 8, 256);
-        fusedEnd = align_up(
-            p.wsFusedPartial + recSlots * p.fusedP * mhc::fused_record_words(n) * 8, 256);
+        p.wsFusedPartial = align_up(p.wsFinal + tiles * mhc::fused_bcast_words(n) * 8, 256);
+        p.wsFusedEnd = align_up(
+            p.wsFusedPartial + tiles * p.fusedP * mhc::fused_record_words(n) * 8, 256);
+    }
+    size_t stripEnd = 0;
+    if (p.stripP > 0) {
+        const size_t ring = static_cast<size_t>(p.stripMaxTeams) * mhc::strip_ring_slots();
+        p.wsStripBcast = mhc::kWsHeaderBytes;
+        p.wsStripRecs = align_up(p.wsStripBcast + ring * mhc::strip_bcast_words() * 8, 256);
+        stripEnd = align_up(p.wsStripRecs + ring * p.stripP * mhc::strip_record_words() * 8, 256);
     }
     size_t rowsEnd = 0;
     if (p.rowsS > 0) {
@@ -524,7 +557,20 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
                                                  static_cast<size_t>(M + 1) * 4,
                            256);
     }
-    p.wsTotal = std::max(std::max(splitEnd, fusedEnd), rowsEnd);
+    switch (p.path) {
+    case mhc::Path::kStrip:
+        p.wsTotal = stripEnd;
+        break;
+    case mhc::Path::kFused:
+        p.wsTotal = std::max(p.wsFusedEnd, splitEnd);
+        break;
+    case mhc::Path::kRows:
+        p.wsTotal = rowsEnd;
+        break;
+    default:
+        p.wsTotal = splitEnd;
+        break;
+    }
     return MHC_STATUS_SUCCESS;
 }
 
@@ -641,10 +687,7 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
         // 32 us at D = 1024, 74 -> 54 us at D = 2304); a single-slice team
         // keeps one, which leaves room for more teams.
         const int perXcd = shape.cus / shape.xcds;
-        int teamsPerXcd = perXcd / (p.stripP + (p.stripP >= 2 ? 2 : 1));
-        if (teamsPerXcd < 1) {
-            teamsPerXcd = perXcd / (p.stripP + 1);
-        }
+        int teamsPerXcd = mhc::strip_teams_per_xcd(p.stripP, perXcd);
         // Teams beyond the rings' capacity would have no slots of their own
         // (teams without tiles write nothing).
         if (teamsPerXcd * shape.xcds > p.stripMaxTeams && p.stripMaxTeams < p.fusedTiles) {
@@ -663,7 +706,14 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
             done = true;
         }
     }
-    if (!done && p.fusedP > 0 && (p.path == mhc::Path::kFused || p.path == mhc::Path::kStrip)) {
+    // A strip executor whose device cannot hold its teams (not the device
+    // phase 1 planned for) falls back only to a layout its workspace holds.
+    const auto fallbackOk = [&](size_t end) { return p.path != mhc::Path::kStrip || end <= p.wsTotal; };
+    if (!done && p.path == mhc::Path::kStrip && !fallbackOk(p.wsFusedEnd) && !fallbackOk(p.wsSplitEnd)) {
+        return MHC_STATUS_UNSUPPORTED_SHAPE;
+    }
+    if (!done && p.fusedP > 0 && (p.path == mhc::Path::kFused || p.path == mhc::Path::kStrip) &&
+        fallbackOk(p.wsFusedEnd)) {
         // The fused path, or the strip path's fallback on a device too small
         // for a strip team.  Teams of fusedP workgroups must be co-resident; a
         // device too small for one team runs the split path instead.
@@ -682,6 +732,9 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
         done = true;
     }
     if (!done) {
+        if (!fallbackOk(p.wsSplitEnd)) {
+            return MHC_STATUS_UNSUPPORTED_SHAPE;
+        }
         err = mhc::launch_split(p, workspace, stream);
     }
     return err == hipSuccess ? MHC_STATUS_SUCCESS : MHC_STATUS_HIP_ERROR;

@@ -101,7 +101,7 @@ struct ColLayout {
     static constexpr int Q = M / 16;
     static constexpr bool kHalfTile = (M % 16) == 8;
     static_assert(M % 16 == 0 || M % 16 == 8, "M = n*n + 2n is 24, 48 or 80");
-    __device__ static void slot(int c, bool &lo, int &j)
+    __device__ __forceinline__ static void slot(int c, bool &lo, int &j)
     {
         const int t = c >> 4, l = c & 15;
         if (t < Q) {

@@ -81,7 +81,8 @@ struct Plan {
     // stripXcds, stripTeamsPerXcd and stripGrid are filled per launch from
     // the device.
     int stripP = 0;
-    int stripMaxTeams = 0;  // teams the workspace's exchange rings are sized for
+    int stripMaxTeams = 0;  // teams the workspace's exchange rings are sized for (those of the
+                            // device phase 1 planned for)
     int stripR = 0;
     int stripXcds = 0;
     int stripTeamsPerXcd = 0;
@@ -109,6 +110,10 @@ struct Plan {
     size_t wsPartial = 0;     // split: [S][T][M+1] partials
     size_t wsFinal = 0;       // fused: per-tile hPre / invRms blocks (tagged words)
     size_t wsFusedPartial = 0;// fused: per-(tile, slice) exchange records (tagged words)
+    size_t wsFusedEnd = 0;    // fused: end of its layout (0: no fused layout)
+    size_t wsSplitEnd = 0;    // split: end of its layout
+    size_t wsStripBcast = 0;  // strip: per-team rings of broadcast blocks (tagged words)
+    size_t wsStripRecs = 0;   // strip: per-team rings of P exchange records (tagged words)
     size_t wsRowsB = 0;       // rows (prep launch): B fragments [K/32][NT][64 lanes] x 16 bytes
     size_t wsRowsPartial = 0; // rows: partials, [rowsS][T][M+1] or [T][rowsS][M+1]
     size_t wsTotal = 0;
@@ -183,8 +188,14 @@ hipError_t launch_stream_probe(const void *src, int64_t readBytes, void *dst, in
 // -1 if the plan has no strip kernel.
 int strip_max_coresident(const Plan &plan, int numCUs);
 
-// Exchange ring slots per team of the strip kernel.
+// Exchange ring slots per team of the strip kernel, and the tagged 8-byte
+// words of one exchange record (per slice) and of one broadcast block.
 int strip_ring_slots();
+int strip_record_words();
+int strip_bcast_words();
+// Teams of P slices (plus their reducers) that cusPerXcd CUs of one XCD
+// hold; 0 when not even one fits.
+int strip_teams_per_xcd(int P, int cusPerXcd);
 // Largest number of slice workgroups per team the strip kernel supports.
 int strip_max_slices();
 // Reducer workgroups per team the strip kernel uses when `available` (>= 1)

@@ -132,7 +132,7 @@ struct ColLayout {
     static constexpr int Q = M / 16;
     static constexpr bool kHalfTile = (M % 16) == 8;
     static_assert(M % 16 == 0 || M % 16 == 8, "M = n*n + 2n is 24, 48 or 80");
-    __device__ static void slot(int c, bool &lo, int &j)
+    __device__ __forceinline__ static void slot(int c, bool &lo, int &j)
     {
         const int t = c >> 4, l = c & 15;
         if (t < Q) {
@@ -1147,8 +1147,8 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t launchId, hip
     a.hPre = p.hasHPre ? p.hPre : nullptr;
     a.status = reinterpret_cast<uint64_t *>(ws);
     a.hdr = ws;
-    a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsFinal);
-    a.recs = reinterpret_cast<uint64_t *>(ws + p.wsFusedPartial);
+    a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsStripBcast);
+    a.recs = reinterpret_cast<uint64_t *>(ws + p.wsStripRecs);
     a.T = p.T;
     a.D = p.D;
     a.K = p.K;
@@ -1192,6 +1192,21 @@ hipError_t launch_strip(const Plan &p, void *workspace, uint32_t launchId, hipSt
 }
 
 int strip_ring_slots() { return kRingSlots; }
+
+int strip_record_words() { return Rec<4>::WORDS; }
+
+int strip_bcast_words() { return Rec<4>::BWORDS; }
+
+int strip_teams_per_xcd(int P, int cusPerXcd)
+{
+    // Teams of two or more slices get at least two reducers; a single-slice
+    // team keeps one, which leaves room for more teams.
+    int t = cusPerXcd / (P + (P >= 2 ? 2 : 1));
+    if (t < 1) {
+        t = cusPerXcd / (P + 1);
+    }
+    return t;
+}
 
 int strip_max_slices() { return kMaxSlices; }
 

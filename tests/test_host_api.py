@@ -76,10 +76,46 @@ def test_valid_call_sizes_workspace(pkg, lib):
     assert _call(pkg, lib, d) == (st, ws)
 
 
-def test_workspace_is_device_independent_and_grows_with_shape(pkg, lib):
-    _, small = _call(pkg, lib, _descs(pkg, S=16))
-    _, big = _call(pkg, lib, _descs(pkg, S=4096))
+def test_workspace_grows_with_shape_on_the_two_pass_paths(pkg, lib):
+    # n = 8, D = 4096 takes the rows path: its partial sums grow with T.
+    _, small = _call(pkg, lib, _descs(pkg, S=512, n=8, D=4096))
+    _, big = _call(pkg, lib, _descs(pkg, S=65536, n=8, D=4096))
+    assert _path(pkg, lib, _descs(pkg, S=512, n=8, D=4096)) == "rows"
+    assert _path(pkg, lib, _descs(pkg, S=65536, n=8, D=4096)) == "rows"
     assert big > small > 0
+
+
+def _strip_workspace(pkg, teams, P):
+    """The strip layout on the planned device (MI355X's shape here, no GPU is
+    visible: 8 XCDs of 32 CUs): the workspace header, then per team a ring
+    of 10 broadcast blocks of 4 x 16 tagged words, then per team 10 slots of
+    P records of 25 x 16 tagged words (8 bytes each), 256-byte aligned."""
+    header = 256 + 4 * 2048
+    up = lambda v: (v + 255) // 256 * 256
+    ring = teams * 10
+    recs = up(header + ring * 64 * 8)
+    return up(recs + ring * P * 400 * 8)
+
+
+@pytest.mark.parametrize("B,S,D,teams", [
+    (1, 8192, 7168, 8),     # the headline prefill shape: one team of 28 slices per XCD
+    (4, 32768, 7168, 8),    # 131072 rows, the reference's largest T: the same rings
+    (1, 8192, 7936, 8),     # 31 slices, the widest strip team
+    (1, 131072, 1024, 40),  # 4 slices and 2 reducers: 5 teams per XCD
+])
+def test_strip_workspace_does_not_grow_with_rows(pkg, lib, B, S, D, teams):
+    """The strip path keeps its exchange in per-team rings: the workspace is
+    the rings of the teams the device holds, whatever T (the fused layout,
+    per row tile, is 46 MB at the headline and 739 MB at 131072 rows)."""
+    d = _descs(pkg, B=B, S=S, D=D)
+    assert _path(pkg, lib, d) == "strip"
+    st, ws = _call(pkg, lib, d)
+    assert st == 0
+    assert ws == _strip_workspace(pkg, teams, D // 256)
+    assert ws <= 10 << 20
+    if (B, S) == (4, 32768):
+        _, head = _call(pkg, lib, _descs(pkg, B=1, S=8192, D=D))
+        assert ws == head
 
 
 @pytest.mark.parametrize("over,want", [
@@ -304,11 +340,11 @@ def test_forced_paths(pkg, lib):
 
 def test_no_alloc_rejects_workspaces_beyond_the_builtin_scratch(pkg, lib):
     """mhcPreNoAlloc checks the executor's workspace size against its 64 MiB
-    built-in array before any HIP call: a plan that needs more (the fused
-    layout of 131072 rows at n=4, D=1024: 8192 row tiles x 4 slices of
-    exchange records) is rejected with MHC_STATUS_SCRATCH_TOO_SMALL, and a
-    NULL executor with MHC_STATUS_NULL_ARGUMENT."""
-    T, n, D = 131072, 4, 1024
+    built-in array before any HIP call: a plan that needs more (the rows
+    path's partial sums of 131072 rows at n=8, D=16384) is rejected with
+    MHC_STATUS_SCRATCH_TOO_SMALL, and a NULL executor with
+    MHC_STATUS_NULL_ARGUMENT."""
+    T, n, D = 131072, 8, 16384
     d = _descs(pkg, B=1, S=T, n=n, D=D)
     mk = lambda v: None if v is None else ctypes.byref(pkg.make_tensor(*v))
     ws, exe = ctypes.c_uint64(0), ctypes.c_void_p(None)
