@@ -226,12 +226,31 @@ MHC_API int mhcPreExecutorDestroy(mhcPreExecutor *executor);
  * Device-side status of this executor's latest launch on `workspace`:
  * MHC_STATUS_SUCCESS, or MHC_STATUS_DEVICE_TIMEOUT if one of its bounded
  * waits between workgroups expired (the outputs of such a launch are not
- * valid).  Synchronizes `stream` first.  No reference counterpart (the
- * reference detects a hang only by the caller's own wait,
- * cloud_runner/probe_e1e2.cpp:295).
+ * valid).  Synchronizes `stream` first.  workspace NULL with workspaceSize 0
+ * reads the current device's built-in workspace, that of mhcPreNoAlloc
+ * launches.  No reference counterpart (the reference detects a hang only by
+ * the caller's own wait, cloud_runner/probe_e1e2.cpp:295).
  */
 MHC_API int mhcPreQueryDeviceStatus(void *workspace, uint64_t workspaceSize,
                             const mhcPreExecutor *executor, hipStream_t stream);
+
+/*
+ * A sticky device status word for the executor's launches, read without an
+ * extra synchronize.  No reference counterpart: for callers that launch
+ * without waiting (graph replays, serving loops) and check for errors at
+ * their own next synchronization.  From the executor's next launch on, a
+ * strip or fused launch whose bounded wait between workgroups expired (its
+ * rows then hold NaN) stores MHC_STATUS_DEVICE_TIMEOUT into *deviceWord, a
+ * 4-byte-aligned word of device memory on the executor's device; nothing
+ * else ever writes it, so the caller zeroes it, reads it after any later
+ * synchronization of its own, and zeroes it again.  One word may serve many
+ * executors.  deviceWord NULL turns it off.  Set it before launching, not
+ * concurrently with launches of the same executor.  Such an expiry needs
+ * another kernel to hold CUs the launch needs (an RCCL kernel on a
+ * communication stream, say) and is turned into a guarantee by
+ * MHCPRE_LAUNCH=cooperative.
+ */
+MHC_API int mhcPreExecutorSetStatusWord(mhcPreExecutor *executor, uint32_t *deviceWord);
 
 /* Human-readable name of a status code (static storage). */
 MHC_API const char *mhcPreStatusString(int status);

@@ -94,6 +94,8 @@ def load_library() -> ctypes.CDLL:
     lib.mhcPreExecutorPath.restype = ctypes.c_int
     lib.mhcPreNoAlloc.argtypes = [exe, ctypes.c_void_p]
     lib.mhcPreNoAlloc.restype = ctypes.c_int
+    lib.mhcPreExecutorSetStatusWord.argtypes = [exe, ctypes.c_void_p]
+    lib.mhcPreExecutorSetStatusWord.restype = ctypes.c_int
     w = ctypes.c_void_p
     lib.mhcPrePrepareWeightsSize.argtypes = [T, T, ctypes.c_int32, P(ctypes.c_uint64)]
     lib.mhcPrePrepareWeightsSize.restype = ctypes.c_int
@@ -341,6 +343,23 @@ class MhcPreOp:
             st = self.lib.mhcPreNoAlloc(self.executor, ctypes.c_void_p(_stream_handle(stream)))
         if st != 0:
             raise MhcPreError("mhcPreNoAlloc", st)
+
+    def set_status_word(self, word) -> None:
+        """mhcPreExecutorSetStatusWord: ``word`` (a device int32 tensor, or
+        None) becomes this executor's sticky status word; a later launch whose
+        bounded wait expires stores MHC_STATUS_DEVICE_TIMEOUT into it.  The
+        tensor must outlive the launches that may write it."""
+        ptr = ctypes.c_void_p(word.data_ptr()) if word is not None else None
+        st = self.lib.mhcPreExecutorSetStatusWord(self.executor, ptr)
+        if st != 0:
+            raise MhcPreError("mhcPreExecutorSetStatusWord", st)
+        self._status_word = word
+
+    def no_alloc_device_status(self, stream=None) -> int:
+        """mhcPreQueryDeviceStatus on the built-in workspace of mhcPreNoAlloc
+        launches (NULL workspace, size 0): synchronizes ``stream``."""
+        return self.lib.mhcPreQueryDeviceStatus(None, ctypes.c_uint64(0), self.executor,
+                                                ctypes.c_void_p(_stream_handle(stream)))
 
     def check(self, stream=None) -> None:
         """Synchronize ``stream`` and raise if this executor's latest launch

@@ -22,6 +22,9 @@
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <map>
+#include <tuple>
+#include <unordered_map>
 
 // Prepared weights: B = gamma (.) phi as bf16 hi + lo MFMA fragments in a
 // caller-owned device buffer (layout of mhc::launch_prepare_b).
@@ -47,6 +50,9 @@ struct mhcPreExecutor {
     // device holds x, else at the first launch); -2 until known.
     std::atomic<int> stripCoresident{-2};
     std::atomic<int> fusedCoresident{-2};
+    // The caller's sticky device status word (mhcPreExecutorSetStatusWord),
+    // or null.
+    std::atomic<uint32_t *> statusWord{nullptr};
 };
 
 namespace {
@@ -140,6 +146,18 @@ bool device_shape(int &device, DeviceShape &out)
 // tell which device that is.
 constexpr DeviceShape kPlanShapeDefault{256, 8};
 
+// Phase-1 knobs for tests and measurement sweeps (MHCPRE_FORCE_PATH,
+// MHCPRE_SPIN_LIMIT, MHCPRE_ROWS_B, MHCPRE_ROWS_PARTIALS) are read only when
+// MHCPRE_TESTING=1: a stray one in a production environment changes nothing.
+const char *test_env(const char *name)
+{
+    const char *gate = std::getenv("MHCPRE_TESTING");
+    if (gate == nullptr || std::strcmp(gate, "1") != 0) {
+        return nullptr;
+    }
+    return std::getenv(name);
+}
+
 // Device that holds the device memory at `p`, or -1 when the runtime cannot
 // tell (host memory, an address no allocation covers, no device visible).
 int device_of(const void *p)
@@ -185,6 +203,60 @@ bool shape_matches(const mhcTensor &t, int64_t count, const int64_t *tail, int n
     }
     return true;
 }
+
+// Phase-1 plan cache (the reference caches its tiling per shape,
+// code/op_host/mhc_pre.cpp:36-51,99-121, in an unlocked global): the plan of
+// a shape, without its tensor pointers, keyed by everything the plan depends
+// on, under a lock.  The test knobs bypass it (MHCPRE_TESTING=1).
+struct PlanKey {
+    int64_t T;
+    int64_t D;
+    int n;
+    int xdtype;
+    int device;
+    uint32_t normEps;
+    uint32_t hcEps;
+    bool hasGamma;
+    bool hasHPre;
+    bool cooperative;
+    bool operator==(const PlanKey &o) const
+    {
+        return T == o.T && D == o.D && n == o.n && xdtype == o.xdtype && device == o.device &&
+               normEps == o.normEps && hcEps == o.hcEps && hasGamma == o.hasGamma &&
+               hasHPre == o.hasHPre && cooperative == o.cooperative;
+    }
+};
+struct PlanKeyHash {
+    size_t operator()(const PlanKey &k) const
+    {
+        uint64_t h = 0x9E3779B97F4A7C15ull;
+        const uint64_t parts[] = {static_cast<uint64_t>(k.T), static_cast<uint64_t>(k.D),
+                                  static_cast<uint64_t>(k.n) | (static_cast<uint64_t>(k.xdtype) << 8) |
+                                      (static_cast<uint64_t>(static_cast<uint32_t>(k.device)) << 16),
+                                  (static_cast<uint64_t>(k.normEps) << 32) | k.hcEps,
+                                  static_cast<uint64_t>(k.hasGamma) | (static_cast<uint64_t>(k.hasHPre) << 1) |
+                                      (static_cast<uint64_t>(k.cooperative) << 2)};
+        for (uint64_t v : parts) {
+            h = (h ^ v) * 0xBF58476D1CE4E5B9ull;
+            h ^= h >> 31;
+        }
+        return static_cast<size_t>(h);
+    }
+};
+constexpr size_t kPlanCacheEntries = 1024;  // cleared when full
+
+std::mutex &plan_cache_mutex()
+{
+    static std::mutex mu;
+    return mu;
+}
+std::unordered_map<PlanKey, mhc::Plan, PlanKeyHash> &plan_cache()
+{
+    static std::unordered_map<PlanKey, mhc::Plan, PlanKeyHash> cache;
+    return cache;
+}
+
+bool testing_knobs() { return test_env("MHCPRE_TESTING") != nullptr; }
 
 int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alpha,
                       const mhcTensor *bias, const mhcTensor *gamma, float normEps, float hcEps,
@@ -297,6 +369,33 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     p.hRes = static_cast<float *>(hRes->data);
     p.hPre = hPre != nullptr ? static_cast<float *>(hPre->data) : nullptr;
 
+    // A cached plan of the same shape: the tensor pointers are this call's.
+    const int planDevice = device_of(p.x);
+    const char *launchEnv = std::getenv("MHCPRE_LAUNCH");
+    PlanKey key{T, D, n, x->dtype, planDevice, 0u, 0u, hasGamma, hPre != nullptr,
+                launchEnv != nullptr && std::strcmp(launchEnv, "cooperative") == 0};
+    std::memcpy(&key.normEps, &normEps, 4);
+    std::memcpy(&key.hcEps, &hcEps, 4);
+    const bool useCache = !testing_knobs();
+    if (useCache) {
+        std::lock_guard<std::mutex> lock(plan_cache_mutex());
+        const auto it = plan_cache().find(key);
+        if (it != plan_cache().end()) {
+            const mhc::Plan bound = p;
+            p = it->second;
+            p.x = bound.x;
+            p.phi = bound.phi;
+            p.alpha = bound.alpha;
+            p.bias = bound.bias;
+            p.gamma = bound.gamma;
+            p.hIn = bound.hIn;
+            p.hPost = bound.hPost;
+            p.hRes = bound.hRes;
+            p.hPre = bound.hPre;
+            return MHC_STATUS_SUCCESS;
+        }
+    }
+
     // Split path plan: enough (row tile, K-slice) workgroups to fill the chip,
     // at least 16 k-steps (4 per wave) per slice.
     const int64_t rowTiles = (T + 15) / 16;
@@ -360,7 +459,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
         p.rowsBlocks = static_cast<int>(blocks);
         p.rowsBFromPhi = blocks <= mhc::kRowsPhiMaxBlocks;
-        if (const char *phiEnv = std::getenv("MHCPRE_ROWS_B")) {
+        if (const char *phiEnv = test_env("MHCPRE_ROWS_B")) {
             if (std::strcmp(phiEnv, "phi") == 0) {
                 p.rowsBFromPhi = true;
             } else if (std::strcmp(phiEnv, "prep") == 0) {
@@ -397,7 +496,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         // S = 4: 10.1 / 10.6; n = 8, D = 8192, T = 5472, S = 11: 280.2 /
         // 282.0).
         p.rowsRowMajor = p.rowsS >= 32;
-        if (const char *layoutEnv = std::getenv("MHCPRE_ROWS_PARTIALS")) {
+        if (const char *layoutEnv = test_env("MHCPRE_ROWS_PARTIALS")) {
             if (std::strcmp(layoutEnv, "rows") == 0) {
                 p.rowsRowMajor = true;
             } else if (std::strcmp(layoutEnv, "ranges") == 0) {
@@ -476,7 +575,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             p.path = mhc::Path::kSplit;
         }
     }
-    if (const char *force = std::getenv("MHCPRE_FORCE_PATH")) {
+    if (const char *force = test_env("MHCPRE_FORCE_PATH")) {
         if (std::strcmp(force, "split") == 0) {
             p.path = mhc::Path::kSplit;
         } else if (std::strcmp(force, "fused") == 0 && p.fusedP > 0) {
@@ -490,7 +589,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     if (const char *launch = std::getenv("MHCPRE_LAUNCH")) {
         p.fusedCooperative = std::strcmp(launch, "cooperative") == 0;
     }
-    if (const char *spin = std::getenv("MHCPRE_SPIN_LIMIT")) {
+    if (const char *spin = test_env("MHCPRE_SPIN_LIMIT")) {
         char *end = nullptr;
         const unsigned long v = std::strtoul(spin, &end, 10);
         if (end != spin && *end == '\0' && v <= 0xFFFFFFFFul) {
@@ -503,7 +602,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     // cannot hold one team takes the fused path (or the split path).
     if (p.stripP > 0) {
         DeviceShape shape = kPlanShapeDefault;
-        const int dev = device_of(p.x);
+        const int dev = planDevice;
         if (dev < 0 || !device_shape_of(dev, shape)) {
             (void)hipGetLastError();
             shape = kPlanShapeDefault;
@@ -571,6 +670,13 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         p.wsTotal = splitEnd;
         break;
     }
+    if (useCache) {
+        std::lock_guard<std::mutex> lock(plan_cache_mutex());
+        if (plan_cache().size() >= kPlanCacheEntries) {
+            plan_cache().clear();
+        }
+        plan_cache().emplace(key, p);
+    }
     return MHC_STATUS_SUCCESS;
 }
 
@@ -637,15 +743,39 @@ int get_workspace(const mhcTensor *x, const mhcTensor *phi, const mhcTensor *alp
 }
 
 // Co-resident workgroups of the executor's strip or fused kernel on the
-// current device: the occupancy query runs once per executor and kernel.
+// current device: the occupancy query runs once per process, device and
+// kernel instance (n, x dtype, prepared weights, fused slice width), and its
+// result is kept in the executor too.
 int cached_coresident(std::atomic<int> &slot, int (*query)(const mhc::Plan &, int),
                       const mhc::Plan &p, int cus)
 {
     int v = slot.load(std::memory_order_relaxed);
+    if (v != -2) {
+        return v;
+    }
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess) {
+        (void)hipGetLastError();
+        return query(p, cus);
+    }
+    using Key = std::tuple<uintptr_t, int, int, bool, bool, int, int>;
+    static std::mutex mu;
+    static std::map<Key, int> known;
+    const Key key{reinterpret_cast<uintptr_t>(query), device, p.n, p.isBf16, p.bprep != nullptr,
+                  p.fusedDw, cus};
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        const auto it = known.find(key);
+        if (it != known.end()) {
+            v = it->second;
+        }
+    }
     if (v == -2) {
         v = query(p, cus);
-        slot.store(v, std::memory_order_relaxed);
+        std::lock_guard<std::mutex> lock(mu);
+        known.emplace(key, v);
     }
+    slot.store(v, std::memory_order_relaxed);
     return v;
 }
 
@@ -697,6 +827,7 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
             cached_coresident(executor->stripCoresident, mhc::strip_max_coresident, p, shape.cus) >=
                 shape.cus) {
             mhc::Plan lp = p;
+            lp.statusWord = executor->statusWord.load(std::memory_order_relaxed);
             lp.stripXcds = shape.xcds;
             lp.stripTeamsPerXcd = teamsPerXcd;
             // Workgroups of a team beyond the slices and reducers leave at once.
@@ -721,6 +852,7 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
             cached_coresident(executor->fusedCoresident, mhc::fused_max_coresident, p, shape.cus);
         if (coresident >= p.fusedP) {
             mhc::Plan lp = p;
+            lp.statusWord = executor->statusWord.load(std::memory_order_relaxed);
             lp.fusedTeams = std::min(coresident, mhc::kMaxEpochGrid) / p.fusedP;
             lp.fusedGrid = lp.fusedTeams * p.fusedP;
             err = mhc::launch_fused(lp, workspace, launchId, stream);
@@ -740,18 +872,27 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
     return err == hipSuccess ? MHC_STATUS_SUCCESS : MHC_STATUS_HIP_ERROR;
 }
 
-// The occupancy queries of a new executor, when the current device is the
-// one that holds its tensors (otherwise its first launch makes them).
+// The occupancy queries of a new executor and the address of the device's
+// built-in workspace (mhcPreNoAlloc), when the current device is the one
+// that holds its tensors (otherwise its first launch makes them): so that a
+// later launch, one under stream capture included, makes neither call.
 void prime_coresident(mhcPreExecutor *ex)
 {
     const mhc::Plan &p = ex->plan;
     int device = -1;
     DeviceShape shape;
-    if (ex->device < 0 || (p.path != mhc::Path::kStrip && p.path != mhc::Path::kFused)) {
+    if (ex->device < 0) {
         return;
     }
     if (!device_shape(device, shape) || device != ex->device) {
         (void)hipGetLastError();
+        return;
+    }
+    void *scratch = nullptr;
+    if (mhc::scratch_address(device, &scratch) != hipSuccess) {
+        (void)hipGetLastError();
+    }
+    if (p.path != mhc::Path::kStrip && p.path != mhc::Path::kFused) {
         return;
     }
     if (p.path == mhc::Path::kStrip) {
@@ -966,6 +1107,18 @@ int mhcPreNoAlloc(mhcPreExecutor *executor, hipStream_t stream)
     return launch_on(ws, executor, stream);
 }
 
+int mhcPreExecutorSetStatusWord(mhcPreExecutor *executor, uint32_t *deviceWord)
+{
+    if (executor == nullptr) {
+        return MHC_STATUS_NULL_ARGUMENT;
+    }
+    if (!aligned(deviceWord, 4)) {
+        return MHC_STATUS_MISALIGNED;
+    }
+    executor->statusWord.store(deviceWord, std::memory_order_relaxed);
+    return MHC_STATUS_SUCCESS;
+}
+
 int mhcPreExecutorDestroy(mhcPreExecutor *executor)
 {
     if (executor == nullptr) {
@@ -980,6 +1133,15 @@ int mhcPreQueryDeviceStatus(void *workspace, uint64_t workspaceSize,
 {
     if (executor == nullptr) {
         return MHC_STATUS_NULL_ARGUMENT;
+    }
+    if (workspace == nullptr && workspaceSize == 0) {
+        // The launches of mhcPreNoAlloc: the current device's built-in array.
+        int device = -1;
+        if (hipGetDevice(&device) != hipSuccess || mhc::scratch_address(device, &workspace) != hipSuccess) {
+            (void)hipGetLastError();
+            return MHC_STATUS_HIP_ERROR;
+        }
+        workspaceSize = mhc::kScratchBytes;
     }
     if (workspace == nullptr || workspaceSize < executor->plan.wsTotal) {
         return MHC_STATUS_WORKSPACE_TOO_SMALL;

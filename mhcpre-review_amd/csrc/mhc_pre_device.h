@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mhc_pre.h"
+
 namespace mhc {
 namespace dev {
 
@@ -237,6 +239,18 @@ __device__ __forceinline__ bool epoch_publish(void *ws, size_t epochOff, size_t 
 
 // Quiet NaN written into the outputs of rows whose exchange wait expired.
 __device__ __forceinline__ float poison() { return __uint_as_float(0x7FC00000u); }
+
+// The caller's sticky status word (mhcPreExecutorSetStatusWord), if set: a
+// workgroup whose bounded wait expired stores the public timeout status in
+// it (a buffer store, device scope); nothing else writes it.
+__device__ __forceinline__ void st_status_word(uint32_t *w)
+{
+    if (w != nullptr) {
+        __builtin_amdgcn_raw_buffer_store_b32(
+            (uint32_t)MHC_STATUS_DEVICE_TIMEOUT,
+            __builtin_amdgcn_make_buffer_rsrc(w, (short)0, 4, 0x00020000), 0, 0, 16 /* sc1 */);
+    }
+}
 
 // Sigmoid in the reference vector order (code/op_kernel/mhc_pre.cpp:542-555):
 // scale, +bias, negate, exp, +1, reciprocal, +eps (only when eps != 0).

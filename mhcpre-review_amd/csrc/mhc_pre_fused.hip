@@ -79,6 +79,7 @@ struct FusedArgs {
     uint64_t *bcast;     // [RT] blocks of Rec<N>::BWORDS tagged words
     uint64_t *status;    // (launchId << 32) | kDeviceTimeout after a timeout
     char *hdr;           // workspace header (status word, exchange epoch)
+    uint32_t *statusWord;  // the caller's sticky status word, or null
     int64_t T;
     int64_t D;
     int64_t K;
@@ -237,6 +238,7 @@ __device__ __forceinline__ void record_timeout(const FusedArgs &a, int lane)
     if (lane == 0) {
         __hip_atomic_store(a.status, ((uint64_t)a.launchId << 32) | kDeviceTimeout, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+        st_status_word(a.statusWord);
     }
 }
 
@@ -785,6 +787,7 @@ hipError_t launch_fused_t(const Plan &p, void *workspace, uint32_t launchId, hip
     a.hRes = p.hRes;
     a.hPre = p.hasHPre ? p.hPre : nullptr;
     a.status = reinterpret_cast<uint64_t *>(ws);
+    a.statusWord = p.statusWord;
     a.hdr = ws;
     a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsFinal);
     a.recs = reinterpret_cast<uint64_t *>(ws + p.wsFusedPartial);

@@ -119,6 +119,7 @@ struct Plan {
     size_t wsTotal = 0;
 
     // Bound device pointers (caller memory).
+    uint32_t *statusWord = nullptr;  // strip / fused launches: the caller's sticky status word
     const void *x = nullptr;
     const float *phi = nullptr;
     const float *alpha = nullptr;

@@ -107,6 +107,7 @@ struct StripArgs {
     uint64_t *bcast;   // [team][ringSlots] blocks of Rec<N>::BWORDS tagged words
     uint64_t *status;  // (launchId << 32) | kDeviceTimeout after a timeout
     char *hdr;         // workspace header (status word, exchange epoch)
+    uint32_t *statusWord;  // the caller's sticky status word, or null
     int64_t T;
     int64_t D;
     int64_t K;
@@ -214,6 +215,7 @@ __device__ __forceinline__ void record_timeout(const StripArgs &a, int lane)
 {
     if (lane == 0) {
         st_status(a.status, a.launchId);
+        st_status_word(a.statusWord);
     }
 }
 
@@ -869,6 +871,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 if (spins >= spinLimit) {
                     if (lane == 0) {
                         st_status(statusW, launchId);
+                        st_status_word(a.statusWord);
                     }
                     timedOut = true;
                     break;
@@ -1114,6 +1117,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         if (!epoch_publish(a.hdr, kWsEpochOff, kWsSeenOff, epoch, (int)gridDim.x, spinLimit) &&
             lane == 0) {
             st_status(statusW, launchId);
+            st_status_word(a.statusWord);
         }
     }
 }
@@ -1147,6 +1151,7 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t launchId, hip
     a.hPre = p.hasHPre ? p.hPre : nullptr;
     a.status = reinterpret_cast<uint64_t *>(ws);
     a.hdr = ws;
+    a.statusWord = p.statusWord;
     a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsStripBcast);
     a.recs = reinterpret_cast<uint64_t *>(ws + p.wsStripRecs);
     a.T = p.T;

@@ -16,6 +16,19 @@ Only device (ROCm "cuda") tensors have a kernel; the fake implementation
 gives shapes and dtypes for tracing (meta / fake tensors, torch.compile).
 There is no CPU implementation and no autograd formula (the reference
 operator is forward-only).
+
+Phase 1 is cheap on a repeated shape: the library caches the plan per shape,
+dtypes, gamma presence, eps and device, and each call only validates and
+binds the new tensors.
+
+Expired waits.  The persistent kernels' workgroups wait on each other with a
+bound; if another kernel holds CUs they need (an RCCL kernel on a
+communication stream, say), a wait can expire and the rows it was for come
+out NaN.  Every executor this module creates reports such a launch in a
+per-device sticky status word (mhcPreExecutorSetStatusWord): read it with
+:func:`device_status` after any synchronization of your own, clear it with
+:func:`clear_device_status`.  MHCPRE_CHECK_STATUS=1 instead synchronizes after
+every call and raises.
 """
 from __future__ import annotations
 
@@ -37,10 +50,42 @@ def _check_status() -> bool:
     return os.environ.get("MHCPRE_CHECK_STATUS", "") not in ("", "0")
 
 
+_STATUS_WORDS: dict = {}
+
+
+def _status_word(device: torch.device) -> torch.Tensor:
+    """The per-device sticky status word of this module's executors (one
+    int32, zero until a launch's bounded wait expires)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    word = _STATUS_WORDS.get(index)
+    if word is None:
+        word = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", index))
+        _STATUS_WORDS[index] = word
+    return word
+
+
+def device_status(device=None) -> int:
+    """0, or MHC_STATUS_DEVICE_TIMEOUT (8) if a launch of this module on
+    ``device`` (default: the current one) left NaN rows since the last
+    :func:`clear_device_status`.  Reading the word waits for the launches
+    enqueued before it on the current stream, as any read of a device tensor
+    does; it adds no synchronization of the op's own."""
+    dev = torch.device("cuda", torch.cuda.current_device() if device is None else
+                       torch.device(device).index)
+    return int(_status_word(dev).item())
+
+
+def clear_device_status(device=None) -> None:
+    dev = torch.device("cuda", torch.cuda.current_device() if device is None else
+                       torch.device(device).index)
+    _status_word(dev).zero_()
+
+
 def _launch(x, phi, alpha, bias, gamma, norm_eps, hc_eps, with_h_pre):
     args = [t.contiguous() for t in (x, phi, alpha, bias)]
     g = gamma.contiguous() if gamma is not None else None
     op = MhcPreOp(*args, g, norm_eps, hc_eps, h_pre=True if with_h_pre else None)
+    op.set_status_word(_status_word(x.device))
     try:
         op.launch(check=_check_status())
     finally:

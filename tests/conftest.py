@@ -1,7 +1,12 @@
+import os
 import sys
 from pathlib import Path
 
 import pytest
+
+# The library reads its phase-1 test knobs (MHCPRE_FORCE_PATH,
+# MHCPRE_SPIN_LIMIT, MHCPRE_ROWS_B, MHCPRE_ROWS_PARTIALS) only under this gate.
+os.environ["MHCPRE_TESTING"] = "1"
 
 ROOT = Path(__file__).resolve().parents[1]
 for p in (str(ROOT), str(ROOT / "tests")):

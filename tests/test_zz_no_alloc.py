@@ -100,3 +100,83 @@ def test_no_alloc_matches_workspace_launch(pkg, orc, device, shapes, path):
                    h_pre.reshape(T, n)[rows], ref["h_pre"], orc)
         assert R == len(ref["h_pre"])
         op.close()
+
+
+def test_no_alloc_status_query_reports_an_expired_wait(pkg, device):
+    """mhcPreQueryDeviceStatus(NULL, 0, ...) reads the built-in workspace of
+    mhcPreNoAlloc launches: MHCPRE_SPIN_LIMIT=0 (a phase-1 test knob; a wait
+    gives up at its first poll that finds the data missing, and the kernel
+    ends normally) makes the strip launch report a timeout there, and a
+    normal executor's later no-alloc launch reports none."""
+    import os
+
+    import torch
+
+    T, n, D = 2048, 4, 7168
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
+    x, phi, alpha, bias, gamma = _case(T, n, D, 930, device)
+    xt = torch.from_numpy(x.view(np.int16)).to(device).view(torch.bfloat16)
+    args = (xt, f(phi), f(alpha), f(bias), f(gamma))
+    os.environ["MHCPRE_SPIN_LIMIT"] = "0"
+    try:
+        bad = pkg.MhcPreOp(*args, h_pre=True)
+    finally:
+        os.environ.pop("MHCPRE_SPIN_LIMIT", None)
+    good = pkg.MhcPreOp(*args, h_pre=True)
+    assert bad.path == "strip" and good.path == "strip"
+    timeout = pkg.binding.STATUS_CODE["MHC_STATUS_DEVICE_TIMEOUT"]
+    _say("[no-alloc] status query, spin limit 0")
+    bad.launch_no_alloc()
+    assert bad.no_alloc_device_status() == timeout
+    good.launch_no_alloc()
+    assert good.no_alloc_device_status() == 0
+    assert not torch.isnan(good.h_in.float()).any()
+    # The word under the first executor's launch id still reads as its timeout.
+    assert bad.no_alloc_device_status() == timeout
+    bad.close()
+    good.close()
+
+
+@pytest.mark.parametrize("T,n,D,path", [(1000, 4, 7168, "strip"), (300, 8, 1024, "rows")])
+def test_no_alloc_launch_in_a_graph(pkg, orc, device, T, n, D, path):
+    """mhcPreNoAlloc captured into a HIP graph (its scratch address is
+    resolved when the executor is created, so the capture makes no symbol
+    lookup) and replayed with new x, with eager copies and synchronizations
+    between the replays: every replay equals an eager no-alloc launch bit
+    for bit and matches the oracle."""
+    import torch
+
+    f = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
+    xs = [_case(T, n, D, 940 + i, device) for i in range(3)]
+    _, phi, alpha, bias, gamma = xs[0]
+    xt = torch.from_numpy(xs[0][0].view(np.int16)).to(device).view(torch.bfloat16)
+    op = pkg.MhcPreOp(xt, f(phi), f(alpha), f(bias), f(gamma), h_pre=True)
+    assert op.path == path
+    _say(f"[no-alloc graph] {path} T={T} n={n} D={D}")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        op.launch_no_alloc()
+    torch.cuda.synchronize()
+    for i in (1, 2, 0, 1):
+        xb = xs[i][0]
+        xt.copy_(torch.from_numpy(xb.view(np.int16)).to(device).view(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert op.no_alloc_device_status() == 0
+        replayed = _outputs(op)
+        h_in, h_post, h_res, h_pre = (t.cpu().numpy() for t in replayed)
+        ref = orc.mhc_pre(xb, True, phi, alpha, bias, gamma)
+        assert_close_f32("hPost", h_post.reshape(T, n), ref["h_post"])
+        assert_close_f32("hRes", h_res.reshape(T, n, n), ref["h_res"])
+        assert_close_f32("hPre", h_pre.reshape(T, n), ref["h_pre"])
+        assert_hin(h_in.view(np.uint16).reshape(T, D), ref["h_in"], xb, True,
+                   h_pre.reshape(T, n), ref["h_pre"], orc)
+        op.launch_no_alloc()
+        torch.cuda.synchronize()
+        eager = _outputs(op)
+        for g, w, name in zip(replayed, eager, ("hIn", "hPost", "hRes", "hPre")):
+            assert torch.equal(g, w), (i, name)
+    del graph
+    op.close()
