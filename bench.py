@@ -148,6 +148,48 @@ def cpu_baseline(x, phi, alpha, bias, gamma, bf16: bool, target_s: float) -> dic
             "cpu_model": cpu_model()}
 
 
+def host_call_cost(pkg, op, x, phi, alpha, bias, gamma, prepared: bool) -> dict:
+    """Host cost of one call, outside the timed region: (a) mhcPre on a
+    prebuilt executor (MhcPreOp.launch), (b) the torch operator
+    torch.ops.mhcpre.mhc_pre, which runs phase 1 (a plan-cache hit after the
+    first call), allocates its outputs and workspace and launches.  For each,
+    the host time per call of 100 calls enqueued back to back (one
+    synchronize after them) and the reference harness's latency (one call +
+    stream synchronize, median of 20).  The operator is not timed with
+    prepared weights (it takes phi and gamma)."""
+    import torch
+
+    def enqueue(fn, n=100):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        return (t1 - t0) / n * 1e6
+
+    def latency(fn):
+        fn()
+        torch.cuda.synchronize()
+        ls = []
+        for _ in range(20):
+            h0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ls.append((time.perf_counter() - h0) * 1e6)
+        ls.sort()
+        return (ls[9] + ls[10]) / 2
+
+    out = {"launch": {"enqueue_us": enqueue(op.launch), "latency_us": latency(op.launch)}}
+    if not prepared:
+        pkg.torch_ops()
+        call = lambda: torch.ops.mhcpre.mhc_pre(x, phi, alpha, bias, gamma)
+        out["torch_op"] = {"enqueue_us": enqueue(call), "latency_us": latency(call)}
+    return out
+
+
 def measured_traffic(workload: str, path: str, prepared: bool = False):
     """HBM bytes per launch for this workload from the committed rocprofv3 PMC
     record (FETCH_SIZE + WRITE_SIZE, scaled by a copy of known size) of the
@@ -326,6 +368,7 @@ def main() -> int:
     lat.sort()
     host_latency = {"min": lat[0], "median": (lat[9] + lat[10]) / 2, "avg": sum(lat) / len(lat),
                     "iterations": 20, "warmup": 1}
+    op_cost = host_call_cost(pkg, op, x, phi, alpha, bias, gamma, args.prepared)
 
     # Cold cache: a 512 MiB scratch write before each event-timed launch
     # evicts the MALL (256 MB) and the L2s; median of 20.
@@ -410,6 +453,7 @@ def main() -> int:
                    "event_pair_min_us": durs[0] * 1e3,
                    "cold_us": cold_us,
                    "host_latency_us": host_latency,
+                   "host_call_us": op_cost,
                    "algorithmic_bytes": b_alg,
                    "traffic_source": traffic["summary"] if traffic else None},
         "roofline": {"bound": "hbm", "timing": "cold" if fits_mall else "warm back-to-back",
