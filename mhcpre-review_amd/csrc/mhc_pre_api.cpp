@@ -37,6 +37,46 @@ struct mhcPreWeights {
     int device = -1;  // device holding the buffer (-1: unknown)
 };
 
+namespace {
+
+// Prepared buffers in use: the (n, K) layout each holds and how many weights
+// handles and executors refer to it.  Preparing a buffer again with another
+// layout while any of them lives would make them read fragments in the wrong
+// order, so it is refused; once none is left the buffer is free again.
+struct BufferLayout {
+    int n;
+    int64_t K;
+    int refs;
+};
+std::mutex g_buffersMu;
+std::unordered_map<const void *, BufferLayout> g_buffers;
+
+bool buffer_acquire(const void *buffer, int n, int64_t K)
+{
+    std::lock_guard<std::mutex> lock(g_buffersMu);
+    auto it = g_buffers.find(buffer);
+    if (it == g_buffers.end()) {
+        g_buffers.emplace(buffer, BufferLayout{n, K, 1});
+        return true;
+    }
+    if (it->second.n != n || it->second.K != K) {
+        return false;
+    }
+    ++it->second.refs;
+    return true;
+}
+
+void buffer_release(const void *buffer)
+{
+    std::lock_guard<std::mutex> lock(g_buffersMu);
+    auto it = g_buffers.find(buffer);
+    if (it != g_buffers.end() && --it->second.refs <= 0) {
+        g_buffers.erase(it);
+    }
+}
+
+}  // namespace
+
 struct mhcPreExecutor {
     mhc::Plan plan;
     // Device that holds x (-1: the runtime could not tell, e.g. no device is
@@ -53,6 +93,8 @@ struct mhcPreExecutor {
     // The caller's sticky device status word (mhcPreExecutorSetStatusWord),
     // or null.
     std::atomic<uint32_t *> statusWord{nullptr};
+    // Prepared-weights buffer this executor reads (registered), or null.
+    const void *preparedBuffer = nullptr;
 };
 
 namespace {
@@ -999,6 +1041,11 @@ int mhcPrePrepareWeights(const mhcTensor *phi, const mhcTensor *gamma, int32_t n
     if (w == nullptr) {
         return MHC_STATUS_HIP_ERROR;
     }
+    // A buffer that live handles or executors read with another layout.
+    if (!buffer_acquire(buffer, n, K)) {
+        delete w;
+        return MHC_STATUS_INVALID_SHAPE;
+    }
     // The launch's status is read back with hipGetLastError: first clear an
     // error an earlier call of the process may have left there.
     (void)hipGetLastError();
@@ -1006,6 +1053,7 @@ int mhcPrePrepareWeights(const mhcTensor *phi, const mhcTensor *gamma, int32_t n
                               hasGamma ? static_cast<const float *>(gamma->data) : nullptr, buffer, K,
                               stream) != hipSuccess) {
         (void)hipGetLastError();
+        buffer_release(buffer);
         delete w;
         return MHC_STATUS_HIP_ERROR;
     }
@@ -1033,6 +1081,7 @@ int mhcPreWeightsDestroy(mhcPreWeights *weights)
     if (weights == nullptr) {
         return MHC_STATUS_NULL_ARGUMENT;
     }
+    buffer_release(weights->buffer);
     delete weights;
     return MHC_STATUS_SUCCESS;
 }
@@ -1076,6 +1125,11 @@ int mhcPreGetWorkspaceSizePrepared(const mhcTensor *x, const mhcPreWeights *weig
     if (ex == nullptr) {
         return MHC_STATUS_HIP_ERROR;
     }
+    if (!buffer_acquire(weights->buffer, weights->n, weights->K)) {
+        delete ex;
+        return MHC_STATUS_INVALID_SHAPE;
+    }
+    ex->preparedBuffer = weights->buffer;
     ex->plan = plan;
     ex->device = device;
     prime_coresident(ex);
@@ -1123,6 +1177,9 @@ int mhcPreExecutorDestroy(mhcPreExecutor *executor)
 {
     if (executor == nullptr) {
         return MHC_STATUS_NULL_ARGUMENT;
+    }
+    if (executor->preparedBuffer != nullptr) {
+        buffer_release(executor->preparedBuffer);
     }
     delete executor;
     return MHC_STATUS_SUCCESS;

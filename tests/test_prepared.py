@@ -176,6 +176,12 @@ def _check_oracle(orc, host, outs, bf16):
     (100, 4, 256, False, False, None, "rows"),    # n = 4 small batch
     (200, 4, 4096, True, True, None, "rows"),     # n = 4 wide small batch
     (100, 8, 2048, False, True, None, "rows"),    # n = 8 wide small batch
+    # strip teams at the headline width (28 slices) and the widest (31), both
+    # x dtypes, several tiles per team and a ragged last tile
+    (1000, 4, 7168, True, True, None, "strip"),
+    (1000, 4, 7168, False, True, None, "strip"),
+    (1000, 4, 7936, True, True, None, "strip"),
+    (1000, 4, 7936, False, False, None, "strip"),
 ])
 def test_prepared_matches_plain(pkg, orc, device, T, n, D, bf16, gamma_on, force, path):
     import torch
@@ -298,4 +304,47 @@ def test_prepared_shape_mismatch_is_rejected(pkg, device):
         pkg.MhcPreOp(x2, None, alpha, bias, None, weights=w)
     assert ei.value.status == code(pkg, "MHC_STATUS_INVALID_SHAPE")
     w.close()
+    torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_reprepare_with_another_layout_is_refused_while_in_use(pkg, device):
+    """A prepared buffer holds the fragments of one (n, K): preparing it again
+    with another layout while a weights handle or an executor still reads it
+    would make those read fragments in the wrong order, so it fails with
+    MHC_STATUS_INVALID_SHAPE; the same layout re-prepares, and once every
+    handle and executor on the buffer is gone another layout is accepted."""
+    import ctypes
+
+    import torch
+
+    lib = pkg.load_library()
+    _, (x, phi, alpha, bias, gamma) = _case(device, 64, 4, 512, True, True, seed=21)
+    _, (_, phi_s, _, _, gamma_s) = _case(device, 64, 4, 256, True, True, seed=22)
+    w = pkg.MhcPreWeights(phi, gamma, 4)
+    op = pkg.MhcPreOp(x, None, alpha, bias, None, weights=w)
+
+    def prepare(phi_t, gamma_t, n):
+        handle = ctypes.c_void_p(None)
+        pd, gd = pkg.binding.tensor_desc(phi_t), pkg.binding.tensor_desc(gamma_t)
+        st = lib.mhcPrePrepareWeights(ctypes.byref(pd), ctypes.byref(gd), ctypes.c_int32(n),
+                                      ctypes.c_void_p(w.buffer.data_ptr()),
+                                      ctypes.c_uint64(w.bytes), ctypes.c_uint64(7), None,
+                                      ctypes.byref(handle))
+        return st, handle
+
+    _say("[prepared] re-prepare with another layout")
+    st, h = prepare(phi_s, gamma_s, 4)  # K = 1024 into a K = 2048 buffer in use
+    assert st == code(pkg, "MHC_STATUS_INVALID_SHAPE") and not h.value
+    st, h = prepare(phi, gamma, 4)  # the same layout: fine
+    assert st == 0 and h.value
+    lib.mhcPreWeightsDestroy(h)
+    w.close()  # the executor still reads the buffer
+    st, h = prepare(phi_s, gamma_s, 4)
+    assert st == code(pkg, "MHC_STATUS_INVALID_SHAPE") and not h.value
+    op.close()
+    torch.cuda.synchronize()
+    st, h = prepare(phi_s, gamma_s, 4)  # nothing reads the buffer any more
+    assert st == 0 and h.value
+    lib.mhcPreWeightsDestroy(h)
     torch.cuda.synchronize()
