@@ -148,6 +148,10 @@ def mhc_pre(x_bits: np.ndarray, is_bf16: bool, phi: np.ndarray, alpha, bias, gam
         _ptr(out["mix"], ctypes.c_float), _ptr(out["inv_rms"], ctypes.c_float), int(nthreads))
     if st != 0:
         raise RuntimeError(f"oracle_mhc_pre failed with {st}")
+    # The inputs (references, not copies), for checks that evaluate the
+    # formula in fp64 beside the oracle.
+    out["inputs"] = {"phi": phi, "alpha": alpha, "bias": bias, "gamma": g,
+                     "norm_eps": float(norm_eps), "hc_eps": float(hc_eps), "rows": rows_arr}
     return out
 
 

@@ -29,6 +29,16 @@ def pytest_terminal_summary(terminalreporter):
             f"hIn vs oracle: {HIN_STATS['beyond']} of {HIN_STATS['elements']} elements beyond "
             f"1 ulp (max {HIN_STATS['max_ulp']} ulp) over {HIN_STATS['checks']} checks, each "
             f"within the hPre-propagation bound")
+    if HIN_STATS["attributed"]:
+        terminalreporter.write_line(
+            f"hIn beyond 1 ulp vs an fp64 evaluation: {HIN_STATS['attributed']} elements, device "
+            f"closer {HIN_STATS['device_closer']}, oracle closer {HIN_STATS['oracle_closer']}, "
+            f"tied {HIN_STATS['tied']}; sum of |hIn - fp64| / |fp64|: device "
+            f"{HIN_STATS['device_hin_l1']:.4g}, oracle {HIN_STATS['oracle_hin_l1']:.4g}; "
+            f"|hPre - fp64| on those rows, max: device {HIN_STATS['device_pre_err']:.3e}, "
+            f"oracle {HIN_STATS['oracle_pre_err']:.3e}, mean: device "
+            f"{HIN_STATS['device_pre_l1'] / max(HIN_STATS['pre_count'], 1):.3e}, oracle "
+            f"{HIN_STATS['oracle_pre_l1'] / max(HIN_STATS['pre_count'], 1):.3e}")
 
 
 @pytest.fixture(scope="session")

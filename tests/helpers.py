@@ -26,8 +26,60 @@ ATOL = 1e-5
 HIN_MAX_ULP = 1
 
 # Use of the hPre-propagation allowance over the session (printed at the end
-# of the run by tests/conftest.py).
-HIN_STATS = {"checks": 0, "elements": 0, "beyond": 0, "max_ulp": 0}
+# of the run by tests/conftest.py), and its attribution: for each element
+# beyond 1 ulp whose check had the oracle's inputs, hIn evaluated in fp64
+# from an fp64 hPre (the formula with no rounding but the inputs'), and which
+# of the device's and the oracle's hIn lies closer to it; and the largest
+# hPre error of each against that fp64 hPre on those rows.
+HIN_STATS = {"checks": 0, "elements": 0, "beyond": 0, "max_ulp": 0,
+             "attributed": 0, "device_closer": 0, "oracle_closer": 0, "tied": 0,
+             "device_pre_err": 0.0, "oracle_pre_err": 0.0,
+             "device_hin_l1": 0.0, "oracle_hin_l1": 0.0,
+             "pre_count": 0, "device_pre_l1": 0.0, "oracle_pre_l1": 0.0}
+
+
+def _pre64(x_bits, is_bf16: bool, inputs: dict, n: int) -> np.ndarray:
+    """hPre of the rows of x in fp64: mix = (x * gamma) . phi_j, invRms =
+    1 / sqrt(sum x^2 / K + normEps), sigmoid(mix * invRms * alphaPre + b) +
+    hcEps, with no intermediate rounding."""
+    R, _, D = x_bits.shape
+    K = n * D
+    xf = _decode16(x_bits, is_bf16).reshape(R, K)
+    phi = np.asarray(inputs["phi"], np.float64).reshape(-1, K)[:n]
+    g = inputs["gamma"]
+    xg = xf * np.asarray(g, np.float64)[None, :] if g is not None else xf
+    mix = xg @ phi.T
+    inv = 1.0 / np.sqrt((xf * xf).sum(1) / K + inputs["norm_eps"])
+    a = np.asarray(inputs["alpha"], np.float64)
+    b = np.asarray(inputs["bias"], np.float64)[:n]
+    return 1.0 / (1.0 + np.exp(-(mix * (inv * a[0])[:, None] + b))) + inputs["hc_eps"]
+
+
+def _attribute(got_bits, want_bits, x_bits, is_bf16, got_pre, want_pre, far, inputs):
+    rows = np.nonzero(far.any(1))[0]
+    n = x_bits.shape[1]
+    pre64 = _pre64(x_bits[rows], is_bf16, inputs, n)                   # [r, n]
+    xf = _decode16(x_bits[rows], is_bf16)                               # [r, n, D]
+    h64 = (pre64[:, :, None] * xf).sum(1)                               # [r, D]
+    f = far[rows]
+    dev = np.abs(_decode16(got_bits[rows], is_bf16) - h64)[f]
+    orc = np.abs(_decode16(want_bits[rows], is_bf16) - h64)[f]
+    HIN_STATS["attributed"] += int(f.sum())
+    HIN_STATS["device_closer"] += int((dev < orc).sum())
+    HIN_STATS["oracle_closer"] += int((orc < dev).sum())
+    HIN_STATS["tied"] += int((dev == orc).sum())
+    # Relative to the fp64 value, so that rows of every scale weigh alike.
+    scale = np.maximum(np.abs(h64[f]), 1e-30)
+    HIN_STATS["device_hin_l1"] += float((dev / scale).sum())
+    HIN_STATS["oracle_hin_l1"] += float((orc / scale).sum())
+    op = np.abs(np.asarray(want_pre, np.float64).reshape(-1, n)[rows] - pre64)
+    HIN_STATS["oracle_pre_err"] = max(HIN_STATS["oracle_pre_err"], float(op.max()))
+    if got_pre is not None:
+        dp = np.abs(np.asarray(got_pre, np.float64)[rows] - pre64)
+        HIN_STATS["device_pre_err"] = max(HIN_STATS["device_pre_err"], float(dp.max()))
+        HIN_STATS["pre_count"] += int(dp.size)
+        HIN_STATS["device_pre_l1"] += float(dp.sum())
+        HIN_STATS["oracle_pre_l1"] += float(op.sum())
 
 
 def ordered16(bits: np.ndarray) -> np.ndarray:
@@ -83,9 +135,11 @@ def _ulp16(bits: np.ndarray, is_bf16: bool) -> np.ndarray:
 
 
 def assert_hin(got_bits, want_bits, x_bits, is_bf16: bool, got_pre, want_pre, orc,
-               max_rare_fraction: float = 1e-3) -> None:
+               max_rare_fraction: float = 1e-3, ref: dict = None) -> None:
     """hIn check (see the module docstring).  got_pre=None when the device did
-    not return hPre: the bound then uses the hPre tolerance instead."""
+    not return hPre: the bound then uses the hPre tolerance instead.  ref, the
+    oracle's result dict for these rows, enables the fp64 attribution of the
+    elements beyond 1 ulp (HIN_STATS)."""
     got_bits = np.ascontiguousarray(got_bits).view(np.uint16)
     want_bits = np.ascontiguousarray(want_bits, dtype=np.uint16)
     R, D = want_bits.shape
@@ -113,6 +167,8 @@ def assert_hin(got_bits, want_bits, x_bits, is_bf16: bool, got_pre, want_pre, or
     HIN_STATS["elements"] += int(far.size)
     HIN_STATS["beyond"] += int(far.sum())
     HIN_STATS["max_ulp"] = max(HIN_STATS["max_ulp"], max_ulp)
+    if far.any() and ref is not None and "inputs" in ref:
+        _attribute(got_bits, want_bits, x_bits, is_bf16, got_pre, want_pre, far, ref["inputs"])
     if far.any():
         xf = np.abs(_decode16(x_bits, is_bf16))                      # [R, n, D]
         n = xf.shape[1]

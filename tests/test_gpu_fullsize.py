@@ -74,7 +74,7 @@ def test_full_size(pkg, orc, device, cfg):
     assert_close_f32("hRes", h_res[rows_t].cpu().numpy(), ref["h_res"])
     assert_close_f32("hPre", h_pre[rows_t].cpu().numpy(), ref["h_pre"])
     assert_hin(h_in[rows_t].cpu().numpy().view(np.uint16), ref["h_in"], x_rows, case.is_bf16,
-               h_pre[rows_t].cpu().numpy(), ref["h_pre"], orc)
+               h_pre[rows_t].cpu().numpy(), ref["h_pre"], orc, ref=ref)
 
     # 2) Every row against an fp64 restatement on the GPU.
     K, M = case.K, case.M

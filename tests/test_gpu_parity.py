@@ -80,7 +80,8 @@ def check(out, ref, x_bits, is_bf16, orc):
     assert_close_f32("hRes", out["h_res"], ref["h_res"])
     if "h_pre" in out:
         assert_close_f32("hPre", out["h_pre"], ref["h_pre"])
-    assert_hin(out["h_in"], ref["h_in"], x_bits, is_bf16, out.get("h_pre"), ref["h_pre"], orc)
+    assert_hin(out["h_in"], ref["h_in"], x_bits, is_bf16, out.get("h_pre"), ref["h_pre"], orc,
+               ref=ref)
 
 
 @pytest.mark.parametrize("cfg,force", [(1, None), (2, None), (4, None), (1, "split"),

@@ -145,7 +145,7 @@ def _run_case(pkg, orc, device, i, c):
         fallback = 0
         for name, key in (("hPre", "h_pre"), ("hPost", "h_post"), ("hRes", "h_res")):
             fallback += close_to_oracle_or_exact(name, out[key], ref[key], exact[key])
-        assert_hin(out["h_in"], ref["h_in"], x, is_bf16, out["h_pre"], ref["h_pre"], orc)
+        assert_hin(out["h_in"], ref["h_in"], x, is_bf16, out["h_pre"], ref["h_pre"], orc, ref=ref)
         if fallback:
             _say(f"[random {i}] {fallback} fp32 outputs held to the fp64 value (oracle off it)")
         paths.append(out["path"])

@@ -303,7 +303,7 @@ def test_rows_subset_and_threads_are_exact(orc):
     full = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma, nthreads=1)
     rows = [127, 0, 64, 3]
     sub = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma, rows=rows, nthreads=4)
-    for k in full:
+    for k in ("h_in", "h_post", "h_res", "h_pre", "mix", "inv_rms"):
         assert np.array_equal(full[k][rows], sub[k]), k
 
 
@@ -330,3 +330,28 @@ def test_weighted_stream_sum_is_the_oracle_hin_stage(orc):
         out = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
         again = orc.weighted_stream_sum(x, case.is_bf16, out["h_pre"])
         assert np.array_equal(again, out["h_in"])
+
+
+@pytest.mark.parametrize("n,D,gamma_on,is_bf16", [(4, 256, True, True), (8, 128, False, False),
+                                                  (6, 64, True, False)])
+def test_fp64_hpre_restatement_matches_the_oracle(orc, n, D, gamma_on, is_bf16):
+    """The fp64 hPre the hIn-allowance attribution uses (tests/helpers.py
+    _pre64) agrees with the oracle's fp32 hPre to fp32 rounding, and moves
+    with alphaPre, the bias, gamma and hcEps as the formula says (a wrong
+    sign, index or eps placement would fail one of these)."""
+    from helpers import _pre64
+
+    rng = np.random.default_rng(1000 + n + D)
+    T, K, M = 40, n * D, n * n + 2 * n
+    x = orc.f32_to_bits(rng.standard_normal((T, n, D)).astype(np.float32), is_bf16)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.asarray([0.7, -0.3, 0.2], np.float32)
+    bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if gamma_on else None
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma, 1e-6, 3e-3)
+    pre64 = _pre64(x, is_bf16, ref["inputs"], n)
+    assert np.allclose(pre64, ref["h_pre"], rtol=2e-6, atol=2e-7)
+    # alpha = 0 leaves sigmoid(bias) + hcEps exactly.
+    inputs = dict(ref["inputs"], alpha=np.asarray([0.0, 1.0, 1.0], np.float32))
+    want = 1.0 / (1.0 + np.exp(-bias[:n].astype(np.float64))) + 3e-3
+    assert np.allclose(_pre64(x, is_bf16, inputs, n), want[None, :], rtol=0, atol=1e-15)

@@ -155,7 +155,7 @@ def _check_oracle(orc, host, outs, bf16):
     assert_close_f32("hRes", h_res.numpy().reshape(T, n, n), ref["h_res"])
     assert_close_f32("hPre", h_pre.numpy().reshape(T, n), ref["h_pre"])
     assert_hin(h_in.view(torch.int16).numpy().view(np.uint16).reshape(T, D), ref["h_in"], x_bits,
-               bf16, h_pre.numpy().reshape(T, n), ref["h_pre"], orc)
+               bf16, h_pre.numpy().reshape(T, n), ref["h_pre"], orc, ref=ref)
 
 
 @pytest.mark.gpu

@@ -97,7 +97,7 @@ def test_no_alloc_matches_workspace_launch(pkg, orc, device, shapes, path):
         assert_close_f32("hRes", h_res.reshape(T, n, n)[rows], ref["h_res"])
         assert_close_f32("hPre", h_pre.reshape(T, n)[rows], ref["h_pre"])
         assert_hin(h_in.view(np.uint16).reshape(T, D)[rows], ref["h_in"], xr, True,
-                   h_pre.reshape(T, n)[rows], ref["h_pre"], orc)
+                   h_pre.reshape(T, n)[rows], ref["h_pre"], orc, ref=ref)
         assert R == len(ref["h_pre"])
         op.close()
 
@@ -172,7 +172,7 @@ def test_no_alloc_launch_in_a_graph(pkg, orc, device, T, n, D, path):
         assert_close_f32("hRes", h_res.reshape(T, n, n), ref["h_res"])
         assert_close_f32("hPre", h_pre.reshape(T, n), ref["h_pre"])
         assert_hin(h_in.view(np.uint16).reshape(T, D), ref["h_in"], xb, True,
-                   h_pre.reshape(T, n), ref["h_pre"], orc)
+                   h_pre.reshape(T, n), ref["h_pre"], orc, ref=ref)
         op.launch_no_alloc()
         torch.cuda.synchronize()
         eager = _outputs(op)
