@@ -103,6 +103,20 @@ CONFIGS = {
 }
 
 
+# The reference's legal extremes (audit_group_vec.py:37,41-45,123-146: any
+# D % 16 == 0 up to 16384 for every n, up to B * S = 4 * 32768 rows) at the
+# shapes that stress this build's paths: n = 4 widths past the strip kernel's
+# 31 slices, the widest n = 4 and n = 6 rows, and the headline width over
+# 131072 rows (x passed as [4, 32768, n, D]).
+EXTREMES = {
+    "n4_D8192_T8192": Case(n=4, D=8192, T=8192, is_bf16=True, gamma=True, seed=20261301),
+    "n4_D16384_T4096": Case(n=4, D=16384, T=4096, is_bf16=True, gamma=True, seed=20261302),
+    "n6_D16384_T4096": Case(n=6, D=16384, T=4096, is_bf16=False, gamma=True, seed=20261303),
+    "n4_D7168_B4_S32768": Case(n=4, D=7168, T=131072, is_bf16=True, gamma=True, seed=20261304),
+}
+EXTREME_LEAD = {"n4_D7168_B4_S32768": (4, 32768)}
+
+
 def outlier_rows(case: Case) -> np.ndarray:
     """Rows scaled x50: splitmix64(seed, 5, r) % 100 == 0, plus the last row."""
     if not case.outliers:

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 from helpers import assert_close_f32, assert_hin
-from inputs import CONFIGS, make_weights, outlier_rows
+from inputs import CONFIGS, EXTREME_LEAD, EXTREMES, make_weights, outlier_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -45,14 +45,27 @@ def _gpu_inputs(case, device):
         f(gamma) if gamma is not None else None), out_rows
 
 
-@pytest.mark.parametrize("cfg", [3, 5])
+@pytest.mark.parametrize("cfg", [3, 5] + sorted(EXTREMES))
 def test_full_size(pkg, orc, device, cfg):
     import torch
 
-    case = CONFIGS[cfg]
-    _say(f"[fullsize] config {cfg}: {case}")
+    case = CONFIGS[cfg] if cfg in CONFIGS else EXTREMES[cfg]
+    _say(f"[fullsize] {cfg}: {case}")
     x, phi, alpha, bias, gamma, pt, at, bt, gt, out_rows = _gpu_inputs(case, device)
-    op = pkg.MhcPreOp(x, pt, at, bt, gt, case.norm_eps, case.hc_eps, h_pre=True)
+    lead = EXTREME_LEAD.get(cfg)
+    if lead is not None:
+        # x as [B, S, n, D] (and outputs of the same leading dims), as the
+        # reference's 4-D contract.
+        x4 = x.view(*lead, case.n, case.D)
+        h_in4 = torch.empty(*lead, case.D, dtype=x.dtype, device=device)
+        op = pkg.MhcPreOp(x4, pt, at, bt, gt, case.norm_eps, case.hc_eps, h_pre=True,
+                          h_in=h_in4)
+        op.h_in = h_in4.view(case.T, case.D)
+        op.h_post = op.h_post.view(case.T, case.n)
+        op.h_res = op.h_res.view(case.T, case.n, case.n)
+        op.h_pre = op.h_pre.view(case.T, case.n)
+    else:
+        op = pkg.MhcPreOp(x, pt, at, bt, gt, case.norm_eps, case.hc_eps, h_pre=True)
     _say(f"[fullsize] path={op.path} workspace={op.workspace_size}")
     op.launch()
     torch.cuda.synchronize()
@@ -62,7 +75,7 @@ def test_full_size(pkg, orc, device, cfg):
     h_post, h_res, h_pre = op.h_post, op.h_res, op.h_pre
 
     # 1) Sampled rows against the CPU oracle.
-    rng = np.random.default_rng(cfg)
+    rng = np.random.default_rng(case.seed)
     rows = np.unique(np.concatenate([
         np.arange(0, 32), np.arange(T - 48, T), rng.choice(T, 192, replace=False), out_rows]))
     rows_t = torch.from_numpy(rows).to(device)
@@ -76,12 +89,17 @@ def test_full_size(pkg, orc, device, cfg):
     assert_hin(h_in[rows_t].cpu().numpy().view(np.uint16), ref["h_in"], x_rows, case.is_bf16,
                h_pre[rows_t].cpu().numpy(), ref["h_pre"], orc, ref=ref)
 
-    # 2) Every row against an fp64 restatement on the GPU.
+    # 2) Every row against an fp64 restatement on the GPU (in row chunks of
+    # at most 16384 rows, to bound its fp64 copy of x).
     K, M = case.K, case.M
-    x64 = x.reshape(T, K).double()
     b64 = pt.double() * (gt.double()[None, :] if gt is not None else 1.0)
-    mix = x64 @ b64.t()
-    inv = 1.0 / torch.sqrt((x64 * x64).sum(1) / K + case.norm_eps)
+    mix = torch.empty((T, M), dtype=torch.float64, device=device)
+    inv = torch.empty((T,), dtype=torch.float64, device=device)
+    for r0 in range(0, T, 16384):
+        x64 = x[r0:r0 + 16384].reshape(-1, K).double()
+        mix[r0:r0 + 16384] = x64 @ b64.t()
+        inv[r0:r0 + 16384] = 1.0 / torch.sqrt((x64 * x64).sum(1) / K + case.norm_eps)
+        del x64
     a = at.double()
     bb = bt.double()
     pre64 = torch.sigmoid(mix[:, :n] * (inv * a[0])[:, None] + bb[:n]) + case.hc_eps
@@ -111,7 +129,7 @@ def test_full_size(pkg, orc, device, cfg):
     neq = int((h_in != want_hin).sum())
     _say(f"[fullsize] hIn rows {T}: {neq} elements differ from the stream sum on the device hPre")
     assert neq == 0, f"hIn: {neq} of {h_in.numel()} elements differ from the reference stream order"
-    del x64, mix
+    del mix
 
     # 3) Relaunch: bitwise identical.
     snap = [t.clone() for t in (h_in, h_post, h_res, h_pre)]
