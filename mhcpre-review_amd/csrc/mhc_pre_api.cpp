@@ -617,7 +617,8 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             p.path = mhc::Path::kSplit;
         }
     }
-    if (const char *force = test_env("MHCPRE_FORCE_PATH")) {
+    const char *force = test_env("MHCPRE_FORCE_PATH");
+    if (force != nullptr) {
         if (std::strcmp(force, "split") == 0) {
             p.path = mhc::Path::kSplit;
         } else if (std::strcmp(force, "fused") == 0 && p.fusedP > 0) {
@@ -649,10 +650,20 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             (void)hipGetLastError();
             shape = kPlanShapeDefault;
         }
-        const int teams = mhc::strip_teams_per_xcd(p.stripP, shape.cus / shape.xcds) * shape.xcds;
+        const int perXcd = shape.cus / shape.xcds;
+        const int teamsPerXcd = mhc::strip_teams_per_xcd(p.stripP, perXcd);
+        const int teams = teamsPerXcd * shape.xcds;
         p.stripMaxTeams = static_cast<int>(std::min<int64_t>(rowTiles, teams));
         if (teams < 1 && p.path == mhc::Path::kStrip) {
             p.path = p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit;
+        }
+        // A team of two or more slices with a single reducer is paced by it
+        // (D = 7936, 31 slices on MI355X's 32 CUs per XCD: 231.9 us at T =
+        // 8192 and 72.3 us at T = 2048, against 193.5 and 62.4 us on the rows
+        // path; 30 slices with two reducers: 123.0 us against 179.5).
+        if (teams >= 1 && p.stripP >= 2 && perXcd / teamsPerXcd - p.stripP < 2 &&
+            p.path == mhc::Path::kStrip && p.rowsS > 0 && force == nullptr) {
+            p.path = mhc::Path::kRows;
         }
     }
 

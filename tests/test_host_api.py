@@ -100,7 +100,7 @@ def _strip_workspace(pkg, teams, P):
 @pytest.mark.parametrize("B,S,D,teams", [
     (1, 8192, 7168, 8),     # the headline prefill shape: one team of 28 slices per XCD
     (4, 32768, 7168, 8),    # 131072 rows, the reference's largest T: the same rings
-    (1, 8192, 7936, 8),     # 31 slices, the widest strip team
+    (1, 8192, 7680, 8),     # 30 slices, the widest strip team with two reducers
     (1, 131072, 1024, 40),  # 4 slices and 2 reducers: 5 teams per XCD
 ])
 def test_strip_workspace_does_not_grow_with_rows(pkg, lib, B, S, D, teams):
@@ -271,6 +271,9 @@ def _path(pkg, lib, d, env=None):
 
 @pytest.mark.parametrize("n,D,S,want", [
     (4, 7168, 4096, "strip"),  # D % 256 == 0, D / 256 <= 31
+    (4, 7680, 8192, "strip"),  # 30 slices and 2 reducers per XCD
+    (4, 7936, 8192, "rows"),   # 31 slices would leave one reducer per team
+    (4, 8192, 8192, "rows"),   # 32 slices do not fit an XCD
     (4, 64, 4096, "split"),    # n = 4, not a strip width: split for K <= 8704 from T = 2048
     (4, 64, 2047, "rows"),
     (4, 2176, 2048, "split"),  # K = 8704

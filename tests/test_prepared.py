@@ -176,12 +176,14 @@ def _check_oracle(orc, host, outs, bf16):
     (100, 4, 256, False, False, None, "rows"),    # n = 4 small batch
     (200, 4, 4096, True, True, None, "rows"),     # n = 4 wide small batch
     (100, 8, 2048, False, True, None, "rows"),    # n = 8 wide small batch
-    # strip teams at the headline width (28 slices) and the widest (31), both
-    # x dtypes, several tiles per team and a ragged last tile
+    # strip teams at the headline width (28 slices) and the widest (30 by
+    # default, 31 forced), both x dtypes, several tiles per team and a ragged
+    # last tile
     (1000, 4, 7168, True, True, None, "strip"),
     (1000, 4, 7168, False, True, None, "strip"),
-    (1000, 4, 7936, True, True, None, "strip"),
-    (1000, 4, 7936, False, False, None, "strip"),
+    (1000, 4, 7680, True, True, None, "strip"),      # 30 slices, the widest default team
+    (1000, 4, 7936, True, True, "strip", "strip"),   # 31 slices (the plan takes rows)
+    (1000, 4, 7936, False, False, "strip", "strip"),
 ])
 def test_prepared_matches_plain(pkg, orc, device, T, n, D, bf16, gamma_on, force, path):
     import torch
