@@ -105,8 +105,8 @@ struct StripArgs {
     float *hPre;
     uint64_t *recs;    // [team][ringSlots][P] records of Rec<N>::WORDS tagged words
     uint64_t *bcast;   // [team][ringSlots] blocks of Rec<N>::BWORDS tagged words
-    uint64_t *status;  // (launchId << 32) | kDeviceTimeout after a timeout
-    char *hdr;         // workspace header (status word, exchange epoch)
+    char *hdr;         // workspace header: the status word ((launchId << 32) |
+                       // kDeviceTimeout after a timeout) at 0, the exchange epoch
     uint32_t *statusWord;  // the caller's sticky status word, or null
     int64_t T;
     int64_t D;
@@ -214,7 +214,7 @@ __device__ __forceinline__ void store16(const u32x4_t &v, __amdgpu_buffer_rsrc_t
 __device__ __forceinline__ void record_timeout(const StripArgs &a, int lane)
 {
     if (lane == 0) {
-        st_status(a.status, a.launchId);
+        st_status(reinterpret_cast<uint64_t *>(a.hdr), a.launchId);
         st_status_word(a.statusWord);
     }
 }
@@ -632,7 +632,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     char *hBase = reinterpret_cast<char *>(a.hIn);
     uint64_t *recsBase = a.recs;
     uint64_t *bcastBase = a.bcast;
-    uint64_t *statusW = a.status;
+    uint64_t *statusW = reinterpret_cast<uint64_t *>(a.hdr);
     int P32 = a.P;
     uint32_t spinLimit = a.spinLimit;
     uint32_t launchId = a.launchId;
@@ -871,7 +871,6 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                 if (spins >= spinLimit) {
                     if (lane == 0) {
                         st_status(statusW, launchId);
-                        st_status_word(a.statusWord);
                     }
                     timedOut = true;
                     break;
@@ -1111,6 +1110,11 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             step(j0, bc, Drain{});
         }
     });
+    // A wave whose wait expired also marks the caller's status word, once,
+    // outside the loop.
+    if (timedOut && lane == 0) {
+        st_status_word(a.statusWord);
+    }
     // Workgroup 0 (always a slice workgroup of team 0) advances the
     // workspace's epoch once every workgroup has taken this one.
     if (g == 0 && w == 0) {
@@ -1149,7 +1153,6 @@ hipError_t launch_strip_t(const Plan &p, void *workspace, uint32_t launchId, hip
     a.hPost = p.hPost;
     a.hRes = p.hRes;
     a.hPre = p.hasHPre ? p.hPre : nullptr;
-    a.status = reinterpret_cast<uint64_t *>(ws);
     a.hdr = ws;
     a.statusWord = p.statusWord;
     a.bcast = reinterpret_cast<uint64_t *>(ws + p.wsStripBcast);
