@@ -228,6 +228,33 @@ def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
     check(out, ref, x, is_bf16, orc)
 
 
+@pytest.mark.parametrize("T,D,is_bf16,has_gamma", [
+    (1024, 4096, True, True),           # 8 tiles per team: 4 own tiles per wave group
+    (1024 - 7, 7168, False, False),     # the same with a ragged last tile
+    (16 * 24 * 7 + 5, 2048, True, True),  # 24 teams of 7 or 8 tiles (own tiles 4 and 3)
+    (16 * 8 * 5, 7168, False, True),    # 5 tiles per team: own tiles 3 and 2
+    (16 * 8 * 9, 4096, True, False),    # 9 tiles per team: own tiles 5 and 4, one whole ring round
+    (16 * 8 + 16, 1024, True, True),    # 40 teams: 9 row tiles, most teams without a tile
+])
+def test_strip_few_tiles_per_team(pkg, orc, device, T, D, is_bf16, has_gamma):
+    """Batches that never wrap the x ring (at most 5 own tiles per wave
+    group): the prologue's two tiles, the steps' loads past the last tile
+    (size-0 resources), the drain steps, and one whole ring round."""
+    n = 4
+    rng = np.random.default_rng(T * 13 + D)
+    K, M = n * D, n * n + 2 * n
+    x = to_bits(rng.standard_normal((T, n, D)).astype(np.float32), is_bf16)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.asarray([0.3, -0.2, 0.05], dtype=np.float32)
+    bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
+    _say(f"[strip-few] T={T} D={D} bf16={is_bf16} gamma={has_gamma}")
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma, force_path="strip")
+    assert out["path"] == "strip"
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
+    check(out, ref, x, is_bf16, orc)
+
+
 def test_attributes_and_hpre_off(pkg, orc, device):
     """Non-default normEps/hcEps (hcEps = 0 skips the add, mhc_pre.cpp:552) and the
     3-output entry point (no hPre)."""
