@@ -690,10 +690,9 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     // Prepared weights (kPrep): the fragments already have this layout; k-step
     // ks of the strip is the prepared k-step (s D + col0 + 32 q) / 32, and the
     // G waves of a strip share its k-steps (the wave of group g copies ks =
-    // g, g + G, ...).  The copy into LDS goes out before the x ring loads, so
-    // that the fragments' registers are free again while the ring fills.
+    // g, g + G, ...); they are copied into LDS below, behind the x loads.
+    u32x4_t pf[kPrep ? KW : 1][kPrep ? NT : 1];
     if constexpr (kPrep) {
-        u32x4_t pf[KW][NT];
 #pragma unroll
         for (int i = 0; i < KW; ++i) {
             const int ks = half + kGroups * i;
@@ -701,13 +700,6 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 pf[i][t] = a.bprep[(gks * NT + t) * 64 + lane];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < KW; ++i) {
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                bfr[half + kGroups * i][t][lane] = pf[i][t];
             }
         }
     } else {
@@ -726,14 +718,27 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // The ring: slot jj mod L holds own tile jj.  Tiles 0 .. L-E-1 are loaded
-    // here, after the phi and gamma loads (which the B build then waits for
-    // without waiting for these); step jj loads tile jj - E + L.
-#pragma unroll
-    for (int b = 0; b < L - E; ++b) {
+    // Every wave's weight loads are in the CU's memory queue before any
+    // wave's x loads.  A wave stalls at a load while the queue is full, and
+    // with each wave's loads in program order, the last waves' weights came
+    // in behind the other waves' first tiles and held the B build (and every
+    // step after it).
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // The ring: slot jj mod L holds own tile jj; tiles 0 .. L-E-1 are loaded
+    // before the first step, and step jj loads tile jj - E + L.  The first
+    // tiles' loads go out in four parts (tile 0 streams 0-1, tile 0 streams
+    // 2-3, then tile 1's), so that a wave stalled at a full memory queue
+    // holds back no more of the B build than one part: with prepared weights
+    // all here, without them one part after each stream's rows are staged
+    // in the B build below (measured at n = 4, D = 7168, T = 8192: the
+    // barrier above ~0.5 us faster per launch, the four parts ~0.7 us more).
+    auto load_x_part = [&](auto pc) __attribute__((always_inline)) {
+        constexpr int part = decltype(pc)::value;
+        constexpr int b = part / 2;
         const __amdgpu_buffer_rsrc_t r = make_rsrc(x_tile(b), rows_of(b) * Ki * 2);
 #pragma unroll
-        for (int s = 0; s < N; ++s) {
+        for (int s = 2 * (part % 2); s < 2 * (part % 2) + 2; ++s) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 xb[b][s][h] = __builtin_bit_cast(
@@ -741,9 +746,21 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                                                                    0, kCpolNt));
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    static_assert(L - E == 2 && N == 4, "the first tiles' loads go out in four parts");
+    if constexpr (kPrep) {
+        static_for<4>(load_x_part);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!kPrep) {  // (prepared fragments were copied above)
+    if constexpr (kPrep) {
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                bfr[half + kGroups * i][t][lane] = pf[i][t];
+            }
+        }
+    } else {
         // One round per stream s, through two staging areas used in turn
         // (the partials buffer, idle until the first step, and stage2): each
         // wave writes its columns' products gamma * phi as bf16 hi and lo
@@ -777,11 +794,19 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             }
         };
         write_rows(0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_x_part(std::integral_constant<int, 0>{});
         lds_barrier();
 #pragma unroll
         for (int s = 0; s < N; ++s) {
             if (s + 1 < N) {
                 write_rows(s + 1);  // the other area: its last reader was round s - 1
+                __builtin_amdgcn_sched_barrier(0);
+                static_for<3>([&](auto pc) __attribute__((always_inline)) {
+                    if (decltype(pc)::value == s) {
+                        load_x_part(std::integral_constant<int, decltype(pc)::value + 1>{});
+                    }
+                });
             }
             const char *stHi = areas[s & 1];
             const char *stLo = stHi + M * kStagePitch;
