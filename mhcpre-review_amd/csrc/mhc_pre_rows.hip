@@ -651,22 +651,6 @@ __global__ __launch_bounds__((small_waves<N, kWide>() * 64)) void rows_small_ker
     const int half = w / kBlocks;                      // its share of the k-steps
     const int kw0 = half * kKsW;                       // first k-step (in the range) it multiplies
 
-    // x as whole 128-byte lines (two k-steps of a row): for pair p, register
-    // (p, h) holds, in lane l, row 16 rb + 8h + (l & 7) and the 8 k at
-    // 8(l >> 4) + 32((l >> 3) & 1) of k-steps kg0 + kw0 + 2p and the next;
-    // a DPP exchange turns each pair into the A fragments of the two.
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, T * K2);
-    constexpr int kPairs = kKsW / 2;
-    u32x4_t xln[kPairs][2];
-#pragma unroll
-    for (int p = 0; p < kPairs; ++p) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            xln[p][h] = load16<kCpolNt>(xr, (16 * rb + 8 * h + (lane & 7)) * K2 +
-                                                (int)((kg0 + kw0 + 2 * p) * 64) + 16 * (lane >> 4) +
-                                                64 * ((lane >> 3) & 1));
-        }
-    }
     // phi rows as whole 256-byte runs (the wave's 64 k of 4 rows per load),
     // into LDS in row order; read back below in B-fragment order.  Prepared
     // weights: the wave's NT fragments of each of its k-steps instead.
@@ -699,7 +683,29 @@ __global__ __launch_bounds__((small_waves<N, kWide>() * 64)) void rows_small_ker
             gm[kk][1] = gsrc[1];
         }
     }
-    // Every load is issued before any use: one memory round trip.
+    // Every wave's weight loads are in the CU's memory queue before any x
+    // load (a wave stalls at a load while the queue is full, so x issued
+    // first held back the B build); every load is issued before any use:
+    // one memory round trip.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // x as whole 128-byte lines (two k-steps of a row): for pair p, register
+    // (p, h) holds, in lane l, row 16 rb + 8h + (l & 7) and the 8 k at
+    // 8(l >> 4) + 32((l >> 3) & 1) of k-steps kg0 + kw0 + 2p and the next;
+    // a DPP exchange turns each pair into the A fragments of the two.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, T * K2);
+    constexpr int kPairs = kKsW / 2;
+    u32x4_t xln[kPairs][2];
+#pragma unroll
+    for (int p = 0; p < kPairs; ++p) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            xln[p][h] = load16<kCpolNt>(xr, (16 * rb + 8 * h + (lane & 7)) * K2 +
+                                                (int)((kg0 + kw0 + 2 * p) * 64) + 16 * (lane >> 4) +
+                                                64 * ((lane >> 3) & 1));
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     if (!builder) {
