@@ -947,37 +947,55 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
     const float biasJ = tid < M ? a.bias[tid] : 0.f;
     const float alphaJ = tid < N ? a.alpha[0] : (tid < 2 * N ? a.alpha[1] : a.alpha[2]);
 
-    // First pass of x loads, issued before the partial sums so that both
-    // round trips overlap.  Octets past the part read other columns' data or
-    // zeros (size-bounded resource) and are not stored.
+    // The first pass of x loads (octets past the part read other columns'
+    // data or zeros, size-bounded resource, and are not stored), issued so
+    // that its round trip overlaps the partial sums': before them in the
+    // narrow variant, after the first batch of them in the wide one (a wave
+    // stalls at a load while the CU's memory queue is full, and the sums are
+    // needed first).
     u32x4_t xv[kEpiOct][N];
+    auto load_x = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int o = 0; o < kEpiOct; ++o) {
+        for (int o = 0; o < kEpiOct; ++o) {
 #pragma unroll
-        for (int s = 0; s < N; ++s) {
-            xv[o][s] = load16<kCpolNt>(xr, xLane + o * (kEpiThreads * 16) + s * Di2);
+            for (int s = 0; s < N; ++s) {
+                xv[o][s] = load16<kCpolNt>(xr, xLane + o * (kEpiThreads * 16) + s * Di2);
+            }
         }
-    }
+    };
 
     // Partial sums: group q sums K-ranges [q*Sg, (q+1)*Sg) of column j in
     // order; the groups are then added in group order.
     const int q = tid / COLS;
     const int j = tid - q * COLS;
+    const int Sg = (a.S + G - 1) / G;
+    const int sBeg = q < G ? q * Sg : 0;
+    const int sEnd = q < G ? min(a.S, sBeg + Sg) : 0;
+    const float *src = a.partial + row * a.rowStride + (q < G ? j : 0);
+    const int64_t stride = a.rangeStride;
+    // Wide variant (small batches with many K-ranges; its use is set by
+    // rows_epilogue_wide): up to kBatch are loaded before the first add (one
+    // memory round trip, where a load per add costs one each), then added in
+    // K-range order.  Slots past the group's range load nothing.
+    constexpr int kBatch = 32;
+    float t0[kEpiThreads >= 1024 ? kBatch : 1];
+    if constexpr (kEpiThreads >= 1024) {
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            t0[i] = sBeg + i < sEnd ? src[(int64_t)(sBeg + i) * stride] : 0.f;
+        }
+    }
+    load_x();
     if (q < G) {
-        const int Sg = (a.S + G - 1) / G;
-        const int sBeg = q * Sg;
-        const int sEnd = min(a.S, sBeg + Sg);
-        const float *src = a.partial + row * a.rowStride + j;
-        const int64_t stride = a.rangeStride;
         float v = 0.f;
         if constexpr (kEpiThreads >= 1024) {
-            // Small batches with many K-ranges (this variant's use is set by
-            // rows_epilogue_wide): up to 32 are loaded before the first add
-            // (one memory round trip, where a load per add costs one each),
-            // then added in K-range order.  Slots past the group's range load
-            // nothing.
-            constexpr int kBatch = 32;
-            for (int sk = sBeg; sk < sEnd; sk += kBatch) {
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) {
+                if (sBeg + i < sEnd) {
+                    v = v + t0[i];
+                }
+            }
+            for (int sk = sBeg + kBatch; sk < sEnd; sk += kBatch) {
                 float t[kBatch];
 #pragma unroll
                 for (int i = 0; i < kBatch; ++i) {
