@@ -666,6 +666,21 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             p.path = mhc::Path::kRows;
         }
     }
+    // n = 4 widths of 31 or more 256-column slices (no strip team with two
+    // reducers fits an XCD) with long batches: the fused kernel reads x once
+    // and beats the rows path's two reads.  Measured on MI355X, bf16, gamma,
+    // back to back (fused / rows, us): T = 8192: D = 7936 181 / 195, 8192
+    // 184 / 223, 8448 210 / 251, 8704 216 / 245, 9216 217 / 263, 10240 249 /
+    // 284, 11264 293 / 308, 12288 310 / 352, 16384 408 / 403; T = 4096: D =
+    // 7936 97 / 103, 8192 100 / 117, 9216 119 / 137, 10240 144 / 144, 12288
+    // 177 / 172; D = 8192, T = 3072 79.8 / 81.5, T = 2048 60.2 / 57.0; D =
+    // 7936, T = 2048 56.1 / 62.3.  Its per-tile records grow with T: up to
+    // 16384 rows (about 105 MB at D = 8192).
+    if (n == 4 && p.fusedDw == 256 && D / 256 >= 31 && D <= 12288 && p.path == mhc::Path::kRows &&
+        force == nullptr && T <= 16384 &&
+        (T >= 3072 || (D == 7936 && T >= 2048)) && (D <= 9216 || T >= 6144)) {
+        p.path = mhc::Path::kFused;
+    }
 
     // Workspace: the header, then the layout of the path the plan takes (a
     // workspace holds one launch at a time).  The split layout holds B

@@ -299,24 +299,6 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
         }
         return;  // no row tile for any wave of this workgroup
     }
-    if (rt < a.RT) {
-        // In flight while the B slice is built.
-        const int lrow = lane & 7;
-        const int lineOff = 8 * (lane >> 4) + 32 * ((lane >> 3) & 1);
-        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + rt * 16 * a.K, tile_rows(rt) * (int)a.K * 2);
-#pragma unroll
-        for (int s = 0; s < N; ++s) {
-#pragma unroll
-            for (int kp = 0; kp < KP; ++kp) {
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    load_line(xrs, (lrow * (int)a.K + lineOff) * 2, (int)a.K, (int)a.D, (int)d0, s,
-                              kp, h);
-                }
-            }
-        }
-    }
-
     // B slice: fragment f = ((s*KS + ks)*NT + ct)*64 + l holds, for lane l,
     // B[k = s*D + d0 + 32ks + 8(l/16) + e][slot 16ct + l%16], e = 0..7.  A
     // thread builds all NT column tiles of one (s, ks, lane) item, so it reads
@@ -391,6 +373,27 @@ __global__ __launch_bounds__(kFusedWaves * 64) void fused_kernel(FusedArgs a)
             }
         }
     }
+    if (rt < a.RT) {
+        // The first unit's x, issued once the B slice is built: a wave stalls
+        // at a load while the CU's memory queue is full, and these loads
+        // issued first held the weights' loads (and the build) behind them
+        // (n = 4, D = 8192, T = 8192: 186.0 -> 184.0 us).
+        const int lrow = lane & 7;
+        const int lineOff = 8 * (lane >> 4) + 32 * ((lane >> 3) & 1);
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x + rt * 16 * a.K, tile_rows(rt) * (int)a.K * 2);
+#pragma unroll
+        for (int s = 0; s < N; ++s) {
+#pragma unroll
+            for (int kp = 0; kp < KP; ++kp) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    load_line(xrs, (lrow * (int)a.K + lineOff) * 2, (int)a.K, (int)a.D, (int)d0, s,
+                              kp, h);
+                }
+            }
+        }
+    }
+
     if (tid == 0) {
         epochSh = epoch_next(prevEpoch);
         epoch_mark(a.hdr, kWsSeenOff, epochSh, g);

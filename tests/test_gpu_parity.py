@@ -229,6 +229,30 @@ def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
 
 
 @pytest.mark.parametrize("T,D,is_bf16,has_gamma", [
+    (2048, 7936, True, True),        # 31 slices: one reducer per strip team, so fused
+    (4096 - 5, 8192, False, False),  # 32 slices, ragged last tile
+    (3072, 9216, True, False),       # 36 slices: teams span XCDs
+    (6144, 10240, False, True),      # 40 slices
+])
+def test_wide_widths_take_the_fused_kernel(pkg, orc, device, T, D, is_bf16, has_gamma):
+    """n = 4 widths of 31 or more 256-column slices with long batches: the
+    plan takes the fused kernel (x read once) instead of the rows path."""
+    n = 4
+    rng = np.random.default_rng(T * 11 + D)
+    K, M = n * D, n * n + 2 * n
+    x = to_bits(rng.standard_normal((T, n, D)).astype(np.float32), is_bf16)
+    phi = (rng.standard_normal((M, K)) / np.sqrt(K)).astype(np.float32)
+    alpha = np.asarray([0.3, -0.2, 0.05], dtype=np.float32)
+    bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
+    _say(f"[wide-fused] T={T} D={D} bf16={is_bf16} gamma={has_gamma}")
+    out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
+    assert out["path"] == "fused"
+    ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
+    check(out, ref, x, is_bf16, orc)
+
+
+@pytest.mark.parametrize("T,D,is_bf16,has_gamma", [
     (1024, 4096, True, True),           # 8 tiles per team: 4 own tiles per wave group
     (1024 - 7, 7168, False, False),     # the same with a ragged last tile
     (16 * 24 * 7 + 5, 2048, True, True),  # 24 teams of 7 or 8 tiles (own tiles 4 and 3)

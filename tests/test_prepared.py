@@ -182,8 +182,11 @@ def _check_oracle(orc, host, outs, bf16):
     (1000, 4, 7168, True, True, None, "strip"),
     (1000, 4, 7168, False, True, None, "strip"),
     (1000, 4, 7680, True, True, None, "strip"),      # 30 slices, the widest default team
-    (1000, 4, 7936, True, True, "strip", "strip"),   # 31 slices (the plan takes rows)
+    (1000, 4, 7936, True, True, "strip", "strip"),   # 31 slices (the plan takes fused or rows)
     (1000, 4, 7936, False, False, "strip", "strip"),
+    # the fused kernel, the plan's path for long batches of 31+ slices
+    (2048, 4, 7936, True, True, None, "fused"),
+    (3072, 4, 8192, False, True, None, "fused"),
 ])
 def test_prepared_matches_plain(pkg, orc, device, T, n, D, bf16, gamma_on, force, path):
     import torch
