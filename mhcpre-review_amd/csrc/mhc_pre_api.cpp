@@ -188,6 +188,29 @@ bool device_shape(int &device, DeviceShape &out)
 // tell which device that is.
 constexpr DeviceShape kPlanShapeDefault{256, 8};
 
+// Where the strip kernel's teams live on a device: inside each XCD while a
+// team of P slices and two reducers fits one (its exchange then stays in the
+// XCD's L2), else across the whole device, its CUs taken as one group (the
+// kernel then stores its exchange words through to memory, device scope).
+struct StripGeometry {
+    int groups;    // XCDs, or 1
+    int perGroup;  // CUs of a group
+    int teams;     // teams per group
+};
+StripGeometry strip_geometry(int P, const DeviceShape &s)
+{
+    const int perXcd = s.cus / s.xcds;
+    if (P + 2 <= perXcd || s.xcds == 1) {
+        return {s.xcds, perXcd, mhc::strip_teams_per_xcd(P, perXcd)};
+    }
+    // Across the device, four reducers per team even where two would leave
+    // room for one more team (MI355X, T = 8192, bf16, gamma, two / four
+    // reducers: D = 10240 (40 slices) 214.7 / 180.7 us, D = 12288 (48) 269.7
+    // / 221.0 us).
+    const int teams4 = s.cus / (P + 4);
+    return {1, s.cus, teams4 >= 1 ? teams4 : mhc::strip_teams_per_xcd(P, s.cus)};
+}
+
 // Phase-1 knobs for tests and measurement sweeps (MHCPRE_FORCE_PATH,
 // MHCPRE_SPIN_LIMIT, MHCPRE_ROWS_B, MHCPRE_ROWS_PARTIALS) are read only when
 // MHCPRE_TESTING=1: a stray one in a production environment changes nothing.
@@ -650,36 +673,13 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             (void)hipGetLastError();
             shape = kPlanShapeDefault;
         }
-        const int perXcd = shape.cus / shape.xcds;
-        const int teamsPerXcd = mhc::strip_teams_per_xcd(p.stripP, perXcd);
-        const int teams = teamsPerXcd * shape.xcds;
+        const StripGeometry geo = strip_geometry(p.stripP, shape);
+        const int teamsPerXcd = geo.teams;
+        const int teams = teamsPerXcd * geo.groups;
         p.stripMaxTeams = static_cast<int>(std::min<int64_t>(rowTiles, teams));
         if (teams < 1 && p.path == mhc::Path::kStrip) {
             p.path = p.fusedP > 0 ? mhc::Path::kFused : mhc::Path::kSplit;
         }
-        // A team of two or more slices with a single reducer is paced by it
-        // (D = 7936, 31 slices on MI355X's 32 CUs per XCD: 231.9 us at T =
-        // 8192 and 72.3 us at T = 2048, against 193.5 and 62.4 us on the rows
-        // path; 30 slices with two reducers: 123.0 us against 179.5).
-        if (teams >= 1 && p.stripP >= 2 && perXcd / teamsPerXcd - p.stripP < 2 &&
-            p.path == mhc::Path::kStrip && p.rowsS > 0 && force == nullptr) {
-            p.path = mhc::Path::kRows;
-        }
-    }
-    // n = 4 widths of 31 or more 256-column slices (no strip team with two
-    // reducers fits an XCD) with long batches: the fused kernel reads x once
-    // and beats the rows path's two reads.  Measured on MI355X, bf16, gamma,
-    // back to back (fused / rows, us): T = 8192: D = 7936 181 / 195, 8192
-    // 184 / 223, 8448 210 / 251, 8704 216 / 245, 9216 217 / 263, 10240 249 /
-    // 284, 11264 293 / 308, 12288 310 / 352, 16384 408 / 403; T = 4096: D =
-    // 7936 97 / 103, 8192 100 / 117, 9216 119 / 137, 10240 144 / 144, 12288
-    // 177 / 172; D = 8192, T = 3072 79.8 / 81.5, T = 2048 60.2 / 57.0; D =
-    // 7936, T = 2048 56.1 / 62.3.  Its per-tile records grow with T: up to
-    // 16384 rows (about 105 MB at D = 8192).
-    if (n == 4 && p.fusedDw == 256 && D / 256 >= 31 && D <= 12288 && p.path == mhc::Path::kRows &&
-        force == nullptr && T <= 16384 &&
-        (T >= 3072 || (D == 7936 && T >= 2048)) && (D <= 9216 || T >= 6144)) {
-        p.path = mhc::Path::kFused;
     }
 
     // Workspace: the header, then the layout of the path the plan takes (a
@@ -884,19 +884,20 @@ int launch_on(void *workspace, mhcPreExecutor *executor, hipStream_t stream)
         // the reducer paces the team (measured on MI355X at T = 8192: 43 ->
         // 32 us at D = 1024, 74 -> 54 us at D = 2304); a single-slice team
         // keeps one, which leaves room for more teams.
-        const int perXcd = shape.cus / shape.xcds;
-        int teamsPerXcd = mhc::strip_teams_per_xcd(p.stripP, perXcd);
+        const StripGeometry geo = strip_geometry(p.stripP, shape);
+        const int perXcd = geo.perGroup;
+        int teamsPerXcd = geo.teams;
         // Teams beyond the rings' capacity would have no slots of their own
         // (teams without tiles write nothing).
-        if (teamsPerXcd * shape.xcds > p.stripMaxTeams && p.stripMaxTeams < p.fusedTiles) {
-            teamsPerXcd = p.stripMaxTeams / shape.xcds;
+        if (teamsPerXcd * geo.groups > p.stripMaxTeams && p.stripMaxTeams < p.fusedTiles) {
+            teamsPerXcd = p.stripMaxTeams / geo.groups;
         }
         if (teamsPerXcd >= 1 && shape.cus <= mhc::kMaxEpochGrid &&
             cached_coresident(executor->stripCoresident, mhc::strip_max_coresident, p, shape.cus) >=
                 shape.cus) {
             mhc::Plan lp = p;
             lp.statusWord = executor->statusWord.load(std::memory_order_relaxed);
-            lp.stripXcds = shape.xcds;
+            lp.stripXcds = geo.groups;
             lp.stripTeamsPerXcd = teamsPerXcd;
             // Workgroups of a team beyond the slices and reducers leave at once.
             lp.stripR = mhc::strip_reducers(perXcd / teamsPerXcd - p.stripP);

@@ -89,7 +89,7 @@ static_assert(kLag < kRing, "ring geometry");
 constexpr int kMaxReducers = 4;
 constexpr int kRingSlots = 2 * kLag + kMaxReducers;
 static_assert(kRingSlots >= (kLag + 1) * kGroups, "ring slots");
-constexpr int kMaxSlices = 31;              // slice workgroups per team (the reducer loads are sized for it)
+constexpr int kMaxSlices = 64;              // slice workgroups per team (the reducer loads are sized for it)
 constexpr int kXccIdReg = (3 << 11) | 20;    // s_getreg operand: HW_REG_XCC_ID, bits [3:0]
 
 struct StripArgs {

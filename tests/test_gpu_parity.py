@@ -205,8 +205,11 @@ def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_ga
 @pytest.mark.parametrize("T,D,is_bf16,has_gamma", [
     (6144 + 5, 1536, True, True),    # P = 6: 4 teams per XCD, 2 reducers each; 12+ steps per team
     (4096, 3584, False, True),       # P = 14: 2 teams per XCD, 2 reducers each
-    (3072 - 3, 7936, True, False),   # P = 31, the largest team: 1 reducer; 24 steps per team
+    (3072 - 3, 7936, True, False),   # P = 31: teams across XCDs (7 teams, 4 reducers)
     (40, 7168, True, True),          # 3 row tiles for 8 teams: most teams have no tile
+    (2048 + 7, 8192, False, True),   # P = 32: teams across XCDs, ragged last tile
+    (1024, 12288, True, True),       # P = 48: 4 teams
+    (64 * 16 * 3 + 16, 16384, False, False),  # P = 64: 3 teams; one team gets an extra tile
 ])
 def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
     """Team geometries of the strip kernel on a 32-CU-per-XCD device: reducer
@@ -229,14 +232,16 @@ def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
 
 
 @pytest.mark.parametrize("T,D,is_bf16,has_gamma", [
-    (2048, 7936, True, True),        # 31 slices: one reducer per strip team, so fused
+    (2048, 7936, True, True),        # 31 slices: 7 teams of 4 reducers across the device
     (4096 - 5, 8192, False, False),  # 32 slices, ragged last tile
-    (3072, 9216, True, False),       # 36 slices: teams span XCDs
-    (6144, 10240, False, True),      # 40 slices
+    (3072, 9216, True, False),       # 36 slices
+    (1500, 10240, False, True),      # 40 slices: 5 teams
+    (700, 16384, True, True),        # 64 slices, the widest team: 3 teams
 ])
-def test_wide_widths_take_the_fused_kernel(pkg, orc, device, T, D, is_bf16, has_gamma):
-    """n = 4 widths of 31 or more 256-column slices with long batches: the
-    plan takes the fused kernel (x read once) instead of the rows path."""
+def test_wide_widths_take_strip_teams_across_xcds(pkg, orc, device, T, D, is_bf16, has_gamma):
+    """n = 4 widths of 31 or more 256-column slices: the strip kernel with
+    teams that span XCDs (their exchange words written through to memory at
+    device scope) instead of the rows path."""
     n = 4
     rng = np.random.default_rng(T * 11 + D)
     K, M = n * D, n * n + 2 * n
@@ -245,9 +250,9 @@ def test_wide_widths_take_the_fused_kernel(pkg, orc, device, T, D, is_bf16, has_
     alpha = np.asarray([0.3, -0.2, 0.05], dtype=np.float32)
     bias = rng.uniform(-0.5, 0.5, M).astype(np.float32)
     gamma = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if has_gamma else None
-    _say(f"[wide-fused] T={T} D={D} bf16={is_bf16} gamma={has_gamma}")
+    _say(f"[wide-strip] T={T} D={D} bf16={is_bf16} gamma={has_gamma}")
     out = run_gpu(pkg, device, x, is_bf16, phi, alpha, bias, gamma)
-    assert out["path"] == "fused"
+    assert out["path"] == "strip"
     ref = orc.mhc_pre(x, is_bf16, phi, alpha, bias, gamma)
     check(out, ref, x, is_bf16, orc)
 

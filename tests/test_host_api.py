@@ -272,20 +272,14 @@ def _path(pkg, lib, d, env=None):
 @pytest.mark.parametrize("n,D,S,want", [
     (4, 7168, 4096, "strip"),  # D % 256 == 0, D / 256 <= 31
     (4, 7680, 8192, "strip"),  # 30 slices and 2 reducers per XCD
-    (4, 7936, 8192, "fused"),  # 31 slices would leave one reducer per team: fused
-    (4, 7936, 2048, "fused"),
-    (4, 7936, 2047, "rows"),
-    (4, 8192, 8192, "fused"),  # 32 slices do not fit an XCD: fused for long batches
-    (4, 8192, 3072, "fused"),
-    (4, 8192, 3071, "rows"),
-    (4, 8192, 16384, "fused"),
-    (4, 8192, 16385, "rows"),  # the fused records grow with T: rows beyond 16384 rows
-    (4, 9216, 3072, "fused"),
-    (4, 10240, 6144, "fused"),
-    (4, 10240, 6143, "rows"),
-    (4, 12288, 8192, "fused"),
-    (4, 12544, 8192, "rows"),  # beyond D = 12288 the rows path is as fast
-    (4, 16384, 8192, "rows"),
+    (4, 7936, 8192, "strip"),  # 31 or more slices: teams across XCDs
+    (4, 7936, 1025, "strip"),
+    (4, 8192, 8192, "strip"),
+    (4, 8192, 512, "strip"),
+    (4, 8192, 256, "rows"),    # small batches stay on the rows path
+    (4, 12288, 8192, "strip"),
+    (4, 16384, 4096, "strip"), # 64 slices, the widest team
+    (4, 16640, 4096, "rows"),  # 65 slices: rows
     (4, 64, 4096, "split"),    # n = 4, not a strip width: split for K <= 8704 from T = 2048
     (4, 64, 2047, "rows"),
     (4, 2176, 2048, "split"),  # K = 8704

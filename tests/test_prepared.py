@@ -182,11 +182,11 @@ def _check_oracle(orc, host, outs, bf16):
     (1000, 4, 7168, True, True, None, "strip"),
     (1000, 4, 7168, False, True, None, "strip"),
     (1000, 4, 7680, True, True, None, "strip"),      # 30 slices, the widest default team
-    (1000, 4, 7936, True, True, "strip", "strip"),   # 31 slices (the plan takes fused or rows)
-    (1000, 4, 7936, False, False, "strip", "strip"),
-    # the fused kernel, the plan's path for long batches of 31+ slices
-    (2048, 4, 7936, True, True, None, "fused"),
-    (3072, 4, 8192, False, True, None, "fused"),
+    (1000, 4, 7936, True, True, None, "strip"),      # 31 slices: teams across XCDs
+    (1000, 4, 7936, False, False, None, "strip"),
+    (1500, 4, 8192, False, True, None, "strip"),     # 32 slices
+    (600, 4, 16384, True, True, None, "strip"),      # 64 slices
+    (2048, 4, 7936, True, True, "fused", "fused"),   # the fused kernel (a fallback)
 ])
 def test_prepared_matches_plain(pkg, orc, device, T, n, D, bf16, gamma_on, force, path):
     import torch
