@@ -664,8 +664,9 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     }
 
     // Strip teams: those the device that holds x runs (MI355X's shape when
-    // the runtime cannot tell), at most one per row tile.  A device whose XCDs
-    // cannot hold one team takes the fused path (or the split path).
+    // the runtime cannot tell), at most one per row tile.  A device that
+    // cannot hold one team, inside an XCD or across them, takes the fused
+    // path (or the split path).
     if (p.stripP > 0) {
         DeviceShape shape = kPlanShapeDefault;
         const int dev = planDevice;

@@ -8,8 +8,10 @@
 // hardware dispatches workgroups round-robin over the X XCDs), so a team's
 // exchange stays inside one XCD's L2.  Results do not depend on where a
 // workgroup actually runs (one placed off its team's XCD writes through to
-// memory); only the speed does.  Team t owns row tiles t, t + numTeams, ...
-// (16 rows each); its k-th tile is its "team step k".
+// memory); only the speed does.  Where P slices and two reducers do not fit
+// one XCD, the host launches with X = 1: teams then span the device and
+// every exchange store writes through to memory.  Team t owns row tiles t,
+// t + numTeams, ... (16 rows each); its k-th tile is its "team step k".
 //
 // Slice workgroup p (8 waves, two per SIMD).  Wave w owns strip w mod 4, the
 // 64 columns [256p + 64(w mod 4), +64) of every stream (256 values of K),
