@@ -188,10 +188,21 @@ bool device_shape(int &device, DeviceShape &out)
 // tell which device that is.
 constexpr DeviceShape kPlanShapeDefault{256, 8};
 
-// Where the strip kernel's teams live on a device: inside each XCD while a
-// team of P slices and two reducers fits one (its exchange then stays in the
-// XCD's L2), else across the whole device, its CUs taken as one group (the
-// kernel then stores its exchange words through to memory, device scope).
+// Where the strip kernel's teams live on a device: inside each XCD (the
+// exchange then stays in the XCD's L2), or across the whole device, its CUs
+// taken as one group (the kernel then stores its exchange words through to
+// memory, device scope), with four reducers per team.  The x stream's rate
+// follows the number of CUs that hold slices, so the teams go across XCDs
+// where that puts at least 15% more CUs on slices, or where a team with two
+// reducers does not fit an XCD.  Measured on MI355X (bf16, gamma, back to
+// back, us, in an XCD / across XCDs): T = 8192: D = 2048 (8 slices) 38.1 /
+// 44.4, 2304 (9) 50.2 / 47.4, 2560 (10) 56.5 / 55.3, 3328 (13) 55.1 / 61.0,
+// 4096 (16) 89.9 / 72.5, 5120 (20) 99.8 / 92.4, 5632 (22) 101.6 / 99.9,
+// 6144 (24) 99.9 / 103.3, 7168 (28) 105.7 / 117.3, 7680 (30) 116.3 / 129.9;
+// T = 1024: D = 2560 14.7 / 15.2, 4096 19.2 / 17.6, 6144 20.6 / 20.7.
+// Across XCDs, four reducers even where two would leave room for one more
+// team (T = 8192, two / four: D = 10240 (40 slices) 214.7 / 180.7 us, D =
+// 12288 (48) 269.7 / 221.0 us).
 struct StripGeometry {
     int groups;    // XCDs, or 1
     int perGroup;  // CUs of a group
@@ -200,15 +211,15 @@ struct StripGeometry {
 StripGeometry strip_geometry(int P, const DeviceShape &s)
 {
     const int perXcd = s.cus / s.xcds;
-    if (P + 2 <= perXcd || s.xcds == 1) {
-        return {s.xcds, perXcd, mhc::strip_teams_per_xcd(P, perXcd)};
+    if (s.xcds == 1) {
+        return {1, s.cus, mhc::strip_teams_per_xcd(P, s.cus)};
     }
-    // Across the device, four reducers per team even where two would leave
-    // room for one more team (MI355X, T = 8192, bf16, gamma, two / four
-    // reducers: D = 10240 (40 slices) 214.7 / 180.7 us, D = 12288 (48) 269.7
-    // / 221.0 us).
-    const int teams4 = s.cus / (P + 4);
-    return {1, s.cus, teams4 >= 1 ? teams4 : mhc::strip_teams_per_xcd(P, s.cus)};
+    const int teamsLocal = P + 2 <= perXcd ? mhc::strip_teams_per_xcd(P, perXcd) : 0;
+    const int teamsAcross = s.cus / (P + 4);
+    if (teamsLocal > 0 && teamsAcross * 100 < teamsLocal * s.xcds * 115) {
+        return {s.xcds, perXcd, teamsLocal};
+    }
+    return {1, s.cus, teamsAcross >= 1 ? teamsAcross : mhc::strip_teams_per_xcd(P, s.cus)};
 }
 
 // Phase-1 knobs for tests and measurement sweeps (MHCPRE_FORCE_PATH,

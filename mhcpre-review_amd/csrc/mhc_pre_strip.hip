@@ -343,7 +343,7 @@ struct ColPoll {
     }
 };
 
-template <int N>
+template <int N, int MaxS>
 __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int ntiles, int r, int R,
                                            bool local, float *lds, uint32_t prevEpoch,
                                            uint32_t *epochSh)
@@ -352,8 +352,8 @@ __device__ __forceinline__ void reducer_wg(const StripArgs &a, int team, int nti
     constexpr int COLS = RC::COLS;
     constexpr int kSg1 = (kWaves * 64) / ((N + 1) * 8);
     constexpr int kSg2 = (kWaves * 64) / ((COLS - N - 1) * 8);
-    using Poll1 = ColPoll<N, 0, N + 1, (kMaxSlices + kSg1 - 1) / kSg1>;
-    using Poll2 = ColPoll<N, N + 1, COLS - N - 1, (kMaxSlices + kSg2 - 1) / kSg2>;
+    using Poll1 = ColPoll<N, 0, N + 1, (MaxS + kSg1 - 1) / kSg1>;
+    using Poll2 = ColPoll<N, N + 1, COLS - N - 1, (MaxS + kSg2 - 1) / kSg2>;
     constexpr int kSums = Poll1::SG * Poll1::ITEMS > Poll2::SG * Poll2::ITEMS ? Poll1::SG * Poll1::ITEMS
                                                                               : Poll2::SG * Poll2::ITEMS;
     float *sums = lds;                // [SG][ITEMS][2] of the current phase
@@ -593,8 +593,22 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const bool local = a.nXcd > 1 && (int)(__builtin_amdgcn_s_getreg(kXccIdReg) & 15) == xcd;
 
     if (role >= a.P) {
-        reducer_wg<N>(a, team, (int)ntiles, role - a.P, a.R, local, &part[0][0][0][0], prevEpoch,
-                      &epochSh);
+        // A reducer instance whose unrolled record loads cover the team and
+        // little more: every poll round runs all of them, predicated, and the
+        // round is on the team's critical path (sized for 64 slices, the
+        // reducers of 30-slice teams ran 13% slower, MI355X, D = 7680, T =
+        // 8192).
+        float *lds = &part[0][0][0][0];
+        const int rr = role - a.P;
+        if (a.P <= 8) {
+            reducer_wg<N, 8>(a, team, (int)ntiles, rr, a.R, local, lds, prevEpoch, &epochSh);
+        } else if (a.P <= 16) {
+            reducer_wg<N, 16>(a, team, (int)ntiles, rr, a.R, local, lds, prevEpoch, &epochSh);
+        } else if (a.P <= 32) {
+            reducer_wg<N, 32>(a, team, (int)ntiles, rr, a.R, local, lds, prevEpoch, &epochSh);
+        } else {
+            reducer_wg<N, kMaxSlices>(a, team, (int)ntiles, rr, a.R, local, lds, prevEpoch, &epochSh);
+        }
         return;
     }
 
