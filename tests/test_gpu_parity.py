@@ -210,12 +210,17 @@ def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_ga
     (2048 + 7, 8192, False, True),   # P = 32: teams across XCDs, ragged last tile
     (1024, 12288, True, True),       # P = 48: 4 teams
     (64 * 16 * 3 + 16, 16384, False, False),  # P = 64: 3 teams; one team gets an extra tile
+    (2000 + 3, 2304, True, True),    # P = 9: 19 teams across XCDs, 4 reducers each
+    (1500, 5120, False, True),       # P = 20: 10 teams across XCDs
+    (2500, 2560, True, False),       # P = 10: 2 teams per XCD, 4 reducers each
+    (3000 + 1, 5632, True, True),    # P = 22: one team per XCD
 ])
 def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
-    """Team geometries of the strip kernel on a 32-CU-per-XCD device: reducer
-    counts 1 and 2 (the exchange ring's size argument covers R = 1, 2, 4),
-    the largest slice count, enough tiles per team to wrap the ring of 10
-    slots several times, and teams without tiles."""
+    """Team geometries of the strip kernel on a device of 8 XCDs x 32 CUs:
+    teams inside an XCD and across XCDs, two and four reducers (the exchange
+    ring's size argument covers R = 1, 2, 4), reducer instances sized for 8,
+    16, 32 and 64 slices, the largest slice count, enough tiles per team to
+    wrap the ring of 10 slots several times, and teams without tiles."""
     n = 4
     rng = np.random.default_rng(T * 7 + D)
     K, M = n * D, n * n + 2 * n
@@ -258,11 +263,11 @@ def test_wide_widths_take_strip_teams_across_xcds(pkg, orc, device, T, D, is_bf1
 
 
 @pytest.mark.parametrize("T,D,is_bf16,has_gamma", [
-    (1024, 4096, True, True),           # 8 tiles per team: 4 own tiles per wave group
-    (1024 - 7, 7168, False, False),     # the same with a ragged last tile
+    (1024, 4096, True, True),           # 12 teams across XCDs: 5 or 6 tiles per team
+    (1024 - 7, 7168, False, False),     # 8 teams: 8 tiles per team, ragged last tile
     (16 * 24 * 7 + 5, 2048, True, True),  # 24 teams of 7 or 8 tiles (own tiles 4 and 3)
     (16 * 8 * 5, 7168, False, True),    # 5 tiles per team: own tiles 3 and 2
-    (16 * 8 * 9, 4096, True, False),    # 9 tiles per team: own tiles 5 and 4, one whole ring round
+    (16 * 8 * 9, 7168, True, False),    # 9 tiles per team: own tiles 5 and 4, one whole ring round
     (16 * 8 + 16, 1024, True, True),    # 40 teams: 9 row tiles, most teams without a tile
 ])
 def test_strip_few_tiles_per_team(pkg, orc, device, T, D, is_bf16, has_gamma):

@@ -118,6 +118,29 @@ def test_strip_workspace_does_not_grow_with_rows(pkg, lib, B, S, D, teams):
         assert ws == head
 
 
+@pytest.mark.parametrize("D,teams", [
+    (2048, 24),   # 8 slices: 3 teams per XCD with 2 reducers (across: 21 teams)
+    (2304, 19),   # 9 slices: across XCDs, 19 teams of 4 reducers (in an XCD: 16)
+    (2560, 16),   # 10 slices: 2 teams per XCD (across: 18, less than 15% more)
+    (4096, 12),   # 16 slices: across XCDs (in an XCD: 8)
+    (5120, 10),   # 20 slices: across XCDs (in an XCD: 8)
+    (5632, 8),    # 22 slices: in an XCD (across: 9)
+    (7168, 8),    # 28 slices: in an XCD, 4 reducers (across: 8)
+    (7680, 8),    # 30 slices: in an XCD, 2 reducers
+    (7936, 7),    # 31 slices: across XCDs only
+    (16384, 3),   # 64 slices
+])
+def test_strip_team_geometry(pkg, lib, D, teams):
+    """Where the strip kernel's teams live: inside an XCD unless teams across
+    XCDs (four reducers each) put at least 15% more CUs on slices, or two
+    reducers do not fit an XCD.  The team count shows in the ring workspace."""
+    d = _descs(pkg, S=8192, D=D)
+    assert _path(pkg, lib, d) == "strip"
+    st, ws = _call(pkg, lib, d)
+    assert st == 0
+    assert ws == _strip_workspace(pkg, teams, D // 256)
+
+
 @pytest.mark.parametrize("over,want", [
     ({"x": (FAKE, 27, [4, 4, 64])}, "MHC_STATUS_SUCCESS"),  # 3-D is accepted
     ({"x": (FAKE, 27, [1, 1, 4, 4, 64])}, "MHC_STATUS_INVALID_SHAPE"),
