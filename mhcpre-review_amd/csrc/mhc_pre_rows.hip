@@ -947,19 +947,29 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
     const float biasJ = tid < M ? a.bias[tid] : 0.f;
     const float alphaJ = tid < N ? a.alpha[0] : (tid < 2 * N ? a.alpha[1] : a.alpha[2]);
 
-    // The first pass of x loads (octets past the part read other columns'
-    // data or zeros, size-bounded resource, and are not stored), issued so
-    // that its round trip overlaps the partial sums': before them in the
-    // narrow variant, after the first batch of them in the wide one (a wave
-    // stalls at a load while the CU's memory queue is full, and the sums are
-    // needed first).
+    // The first pass of x loads, issued so that its round trip overlaps the
+    // partial sums': before them in the narrow variant, after the first
+    // batch of them in the wide one (a wave stalls at a load while the CU's
+    // memory queue is full, and the sums are needed first).  In the wide
+    // variant threads past the part's octets load nothing (with a row split
+    // over parts, most of its threads: n = 8, D = 7168, T = 64 14.8 -> 14.1
+    // us); the narrow one loads them (other columns' data or zeros,
+    // size-bounded resource, not stored) rather than branch around its
+    // loads (n = 8, D = 8192, T = 5472: 281.1 against 282.2 us).
     u32x4_t xv[kEpiOct][N];
     auto load_x = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int o = 0; o < kEpiOct; ++o) {
+            if (kEpiThreads < 1024 || oBeg + tid + (int64_t)o * kEpiThreads < oEnd) {
 #pragma unroll
-            for (int s = 0; s < N; ++s) {
-                xv[o][s] = load16<kCpolNt>(xr, xLane + o * (kEpiThreads * 16) + s * Di2);
+                for (int s = 0; s < N; ++s) {
+                    xv[o][s] = load16<kCpolNt>(xr, xLane + o * (kEpiThreads * 16) + s * Di2);
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < N; ++s) {
+                    xv[o][s] = u32x4_t{0u, 0u, 0u, 0u};
+                }
             }
         }
     };
@@ -1070,9 +1080,11 @@ __global__ __launch_bounds__(kEpiThreads) void rows_epilogue_kernel(RowsEpiArgs 
         if (base > 0) {
 #pragma unroll
             for (int o = 0; o < kEpiOct; ++o) {
+                if (kEpiThreads < 1024 || oBeg + base + tid + (int64_t)o * kEpiThreads < oEnd) {
 #pragma unroll
-                for (int s = 0; s < N; ++s) {
-                    xv[o][s] = load16<kCpolNt>(xr, (int)(base * 16) + xLane + o * (kEpiThreads * 16) + s * Di2);
+                    for (int s = 0; s < N; ++s) {
+                        xv[o][s] = load16<kCpolNt>(xr, (int)(base * 16) + xLane + o * (kEpiThreads * 16) + s * Di2);
+                    }
                 }
             }
         }
