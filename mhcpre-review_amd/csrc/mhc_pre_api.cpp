@@ -534,7 +534,14 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             }
         }
         p.rowsBlocks = static_cast<int>(blocks);
-        p.rowsBFromPhi = blocks <= mhc::kRowsPhiMaxBlocks;
+        // n = 8 with fp16 x takes the prep launch at every batch: its block
+        // GEMM building B itself needs more registers than two waves per
+        // SIMD have (a 40-byte private segment) and ran slower (MI355X, back
+        // to back, us, in-GEMM / prep: D = 7168, T = 2048 130.4 / 120.1; D =
+        // 8192, T = 1024 82.3 / 80.4, T = 2048 144.7 / 141.5, T = 4096 264.6
+        // / 255.7; D = 4096, T = 2048 89.2 / 83.4; bf16, D = 8192, T = 2048
+        // 122.4 / 133.5 keeps the in-GEMM build).
+        p.rowsBFromPhi = blocks <= mhc::kRowsPhiMaxBlocks && !(n == 8 && !p.isBf16);
         if (const char *phiEnv = test_env("MHCPRE_ROWS_B")) {
             if (std::strcmp(phiEnv, "phi") == 0) {
                 p.rowsBFromPhi = true;
