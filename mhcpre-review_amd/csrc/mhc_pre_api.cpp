@@ -590,20 +590,26 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
     if (n == 4) {
         // The strip kernel where it applies (D % 256 == 0), except small
         // batches: its fixed cost (every workgroup builds its B slice) is
-        // ~12 us whatever the shape, while the rows path's two short
+        // ~11-12 us whatever the shape, while the rows path's two short
         // launches grow with K and T.  Measured on MI355X (back to back, us,
         // bf16 with gamma unless noted, rows / strip): T <= 128 rows at every
-        // width (D = 7168: T = 64 10.4 / 12.2, T = 128 11.8 / 12.4; fp16
-        // without gamma T = 96 11.9 / 12.6, T = 128 12.9 / 12.6, the one
-        // loss); T = 160 rows up to D = 6144 (13.0 / 13.2); up to T = 256
-        // rows from D = 4096, on the wide small-batch GEMM (D = 7168, T =
-        // 160 11.8 / 13.6, T = 256 13.1 / 13.9; D = 4096, T = 192 11.4 /
-        // 12.7, T = 256 12.3 / 13.0) and below while T * D <= 2^19 (D =
-        // 2048, T = 256 11.6 / 12.3; D = 3072, T = 192 12.1 / 12.3 stays
-        // strip); up to T = 1024 while T * D <= 3 * 2^17
-        // (D = 768, T = 512 11.5 / 11.7; D = 256, T = 1024 10.8 / 11.9;
-        // D = 512, T = 1024 12.4 / 11.7 and D = 1024, T = 512 12.5 / 12.3
-        // stay strip).
+        // width (D = 7168: T = 128 10.2 / 11.6; D = 4096, T = 128 9.8 / 11.5;
+        // fp16 without gamma, D = 7168, T = 128 10.8 / 12.4); T = 160 rows
+        // up to D = 6144 (11.3 / 11.9); up to T = 256 rows on the wide
+        // small-batch GEMM at 31 or more slices (their few teams span the
+        // XCDs: D = 7936, T = 256 13.9 / 14.9; D = 8192, T = 256 14.8 / 14.7;
+        // D = 10240, T = 192 14.1 / 15.5; D = 16384, T = 256 20.0 / 20.7;
+        // strip from T = 384: D = 8192 19.0 / 15.4) and below them while T *
+        // D <= 9 * 2^17 (D = 4096, T = 256 12.0 /
+        // 12.3; D = 5120, T = 224 12.2 / 12.8; D = 6144, T = 192 12.0 / 12.1;
+        // D = 7168, T = 160 12.0 / 12.0; strip above: D = 5120, T = 256 12.8
+        // / 12.3; D = 6144, T = 224 12.7 / 11.6; D = 7168, T = 192 12.4 /
+        // 12.3, T = 256 13.5 / 12.3; fp16 without gamma, D = 7168, T = 256
+        // 15.2 / 13.7) and below while T * D <= 2^19 (D = 2048, T = 256 11.0
+        // / 10.9; D = 3072, T = 192 12.1 / 12.3 stays strip); up to T = 1024
+        // while T * D <= 3 * 2^17 (D = 768, T = 512 10.7 / 10.9; D = 256, T =
+        // 768 10.1 / 10.6; D = 256, T = 1024 10.8 / 10.6, D = 512, T = 1024
+        // 11.9 / 10.9 and D = 1024, T = 512 11.7 / 11.0 stay strip).
         //
         // Other widths take the rows path, or the split path for short rows
         // (K <= 8704) from T = 2048, whose 16-row tiles then beat the rows
@@ -616,18 +622,16 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         // T = 8192 35.2 / 17.5 / 21.5) and stays the fallback of shapes the
         // rows path cannot hold.
         if (p.stripP > 0) {
+            // Single-slice teams (D = 256) included: the strip kernel also
+            // beats the split path there (strip / split, us: T = 4096 11.8 /
+            // 13.3, 8192 17.1 / 20.2, 32768 42.7 / 49.6).
             p.path = mhc::Path::kStrip;
-            // One slice per team (D = 256) from T = 4096: the split path
-            // streams faster (strip / split, us: T = 4096 14.5 / 13.8, 8192
-            // 21.5 / 20.2, 32768 55.9 / 49.8; D = 512, T = 8192 22.8 / 28.3
-            // stays strip).
-            if (D == 256 && T >= 4096) {
-                p.path = mhc::Path::kSplit;
-            }
             const int64_t td = T * D;
-            if (p.rowsS > 0 && (T <= 128 || (T <= 160 && D <= 6144) ||
-                                (T <= 256 && (p.rowsSmall || td <= (int64_t{1} << 19))) ||
-                                (T <= 1024 && td <= 3 * (int64_t{1} << 17)))) {
+            if (p.rowsS > 0 &&
+                (T <= 128 || (T <= 160 && D <= 6144) ||
+                 (T <= 256 && ((p.rowsSmall && (td <= 9 * (int64_t{1} << 17) || p.stripP >= 31)) ||
+                               td <= (int64_t{1} << 19))) ||
+                 (T <= 1024 && td <= 3 * (int64_t{1} << 17)))) {
                 p.path = mhc::Path::kRows;
             }
         } else if (p.rowsS > 0) {

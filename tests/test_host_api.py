@@ -316,9 +316,17 @@ def _path(pkg, lib, d, env=None):
     (4, 5632, 1, "rows"),
     (4, 4096, 160, "rows"),    # T <= 160 up to D = 6144
     (4, 6144, 160, "rows"),
-    (4, 7168, 129, "rows"),    # T <= 256 from D = 4096: the wide small-batch GEMM
-    (4, 7168, 256, "rows"),
+    (4, 7168, 129, "rows"),    # T <= 256 on the wide small-batch GEMM while T * D <= 9 * 2^17
+    (4, 7168, 192, "strip"),
+    (4, 7168, 256, "strip"),
     (4, 4096, 256, "rows"),
+    (4, 5120, 224, "rows"),
+    (4, 5120, 256, "strip"),
+    (4, 6144, 192, "rows"),
+    (4, 6144, 224, "strip"),
+    (4, 7936, 256, "rows"),    # ... or at 31 or more slices
+    (4, 16384, 256, "rows"),
+    (4, 16384, 257, "strip"),
     (4, 7168, 257, "strip"),
     (4, 3584, 161, "strip"),   # T <= 256 below D = 4096: rows while T * D <= 2^19
     (4, 2048, 256, "rows"),
@@ -329,7 +337,8 @@ def _path(pkg, lib, d, env=None):
     (4, 256, 1024, "rows"),
     (4, 256, 1025, "strip"),
     (4, 256, 4095, "strip"),
-    (4, 256, 4096, "split"),   # one slice per team from T = 4096
+    (4, 256, 4096, "strip"),   # one slice per team: strip at every longer batch
+    (4, 256, 32768, "strip"),
     (4, 512, 8192, "strip"),
     (4, 512, 1024, "strip"),
     (4, 5696, 64, "rows"),     # not a strip width: rows, not fused
