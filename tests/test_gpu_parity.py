@@ -214,6 +214,11 @@ def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_ga
     (1500, 5120, False, True),       # P = 20: 10 teams across XCDs
     (2500, 2560, True, False),       # P = 10: 2 teams per XCD, 4 reducers each
     (3000 + 1, 5632, True, True),    # P = 22: one team per XCD
+    (4096 + 3, 256, True, True),     # P = 1: 80 single-slice teams of 2 reducers (the default from T = 1025)
+    (5000 + 1, 256, False, False),
+    (777, 3840, True, True),         # P = 15: 13 teams across XCDs
+    (1234, 4352, False, False),      # P = 17: 12 teams across XCDs, reducers sized for 32 slices
+    (2222, 4864, True, False),       # P = 19: 11 teams across XCDs
 ])
 def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
     """Team geometries of the strip kernel on a device of 8 XCDs x 32 CUs:

@@ -124,6 +124,8 @@ def test_strip_workspace_does_not_grow_with_rows(pkg, lib, B, S, D, teams):
     (2560, 16),   # 10 slices: 2 teams per XCD (across: 18, less than 15% more)
     (4096, 12),   # 16 slices: across XCDs (in an XCD: 8)
     (5120, 10),   # 20 slices: across XCDs (in an XCD: 8)
+    (3840, 13),   # 15 slices: across XCDs (in an XCD: 8)
+    (5376, 10),   # 21 slices: across XCDs (in an XCD: 8)
     (5632, 8),    # 22 slices: in an XCD (across: 9)
     (7168, 8),    # 28 slices: in an XCD, 4 reducers (across: 8)
     (7680, 8),    # 30 slices: in an XCD, 2 reducers
