@@ -496,10 +496,19 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             }
         }
     }
-    // Strip path (n = 4): slices of 256 columns, at most strip_max_slices()
-    // of them; its tile and row indices are 32-bit, which bounds T.
-    if (n == 4 && (D % 256) == 0 && D / 256 <= mhc::strip_max_slices() && T < (int64_t{1} << 24)) {
-        p.stripP = static_cast<int>(D / 256);
+    // Strip path (n = 4, D % 64 == 0 from D = 192): slices of 256 columns
+    // (the last one 64, 128 or 192 wide when D % 256 != 0), at most
+    // strip_max_slices() of them; its tile and row indices are 32-bit, which
+    // bounds T.  Measured on MI355X (bf16, gamma, back to back, us, strip /
+    // rows / split): T = 8192: D = 7104 107.4 / 167.5 / 264.6, 4160 75.3 /
+    // 109.0 / 144.2, 2112 47.1 / 65.1 / 65.7, 1216 29.9 / 48.3 / 44.6, 320
+    // 19.3 / 34.4 / 21.6, 192 16.6 / 31.9 / 17.7; T = 2048: D = 7104 33.8 /
+    // 50.7 / 61.1, 1216 14.4 / 21.4 / 19.1, 192 10.2 / 13.7 / 11.7.  One
+    // slice of one or two strips gains nothing on the split path (D = 64,
+    // T = 8192 16.0 / 27.3 / 15.0; D = 128 16.2 / 31.8 / 15.9).
+    if (n == 4 && (D % 64) == 0 && D >= 192 && (D + 255) / 256 <= mhc::strip_max_slices() &&
+        T < (int64_t{1} << 24)) {
+        p.stripP = static_cast<int>((D + 255) / 256);
     }
     // Rows path (any n, K % 128 == 0): rows_block_rows()-row blocks x S
     // K-ranges of contiguous stages (the last range may be shorter).  S balances whole waves of 256
@@ -588,7 +597,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
     }
     if (n == 4) {
-        // The strip kernel where it applies (D % 256 == 0), except small
+        // The strip kernel where it applies (D % 64 == 0, D >= 192), except small
         // batches: its fixed cost (every workgroup builds its B slice) is
         // ~11-12 us whatever the shape, while the rows path's two short
         // launches grow with K and T.  Measured on MI355X (back to back, us,

@@ -1,10 +1,11 @@
-// Strip kernel for gfx950 (n = 4, D % 256 == 0): x is read from HBM once,
+// Strip kernel for gfx950 (n = 4, D % 64 == 0): x is read from HBM once,
 // held in VGPRs in a ring of row tiles until its hIn is written, and the
 // cross-workgroup exchange of the K-reduction runs in the shadow of the x
 // stream.
 //
-// Teams.  The workgroups of one XCD form teams of P = D / 256 slice
-// workgroups and R reducer workgroups.  Workgroup g runs on XCD g mod X (the
+// Teams.  The workgroups of one XCD form teams of P = ceil(D / 256) slice
+// workgroups and R reducer workgroups (the last slice's strips past D, when
+// D % 256 != 0, load zeros and store nothing).  Workgroup g runs on XCD g mod X (the
 // hardware dispatches workgroups round-robin over the X XCDs), so a team's
 // exchange stays inside one XCD's L2.  Results do not depend on where a
 // workgroup actually runs (one placed off its team's XCD writes through to
@@ -623,6 +624,10 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const int Ki = (int)a.K;
     const int Di = (int)a.D;
     const int col0 = p * kSlice + strip * kStripCols;
+    // A strip past D (the last slice when D % 256 != 0) holds no columns:
+    // its x reads zeros through size-0 resources, its B is zero and it
+    // stores no hIn, so it adds nothing to the slice's partial sums.
+    const bool stripLive = col0 < Di;
     const int lrow = lane & 7;
     const int lineOff = 8 * (lane >> 4) + 32 * ((lane >> 3) & 1);
     const int xLane = (lrow * Ki + col0 + lineOff) * 2;
@@ -715,22 +720,27 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
             const int64_t gks = ((int64_t)(ks >> 1) * a.D + col0 + 32 * (ks & 1)) / 32;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                pf[i][t] = a.bprep[(gks * NT + t) * 64 + lane];
+                pf[i][t] = stripLive ? a.bprep[(gks * NT + t) * 64 + lane] : u32x4_t{0u, 0u, 0u, 0u};
             }
         }
     } else {
         const __amdgpu_buffer_rsrc_t phiR = make_rsrc(a.phi, M * Ki * 4);
         const __amdgpu_buffer_rsrc_t gamR = make_rsrc(a.gamma, hasGamma ? Ki * 4 : 0);
+        // Lanes whose 4 values of K lie past D read zeros (offsets past the
+        // resources' ends).
+        const bool laneLive = p * kSlice + 4 * lane < Di;
 #pragma unroll
         for (int s = 0; s < N; ++s) {
 #pragma unroll
             for (int c = 0; c < CPW; ++c) {
                 pv[s][c] = __builtin_bit_cast(
                     f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                 phiR, ((CPW * w + c) * Ki + s * Di + p * kSlice) * 4 + 16 * lane, 0, 0));
+                                 phiR, laneLive ? ((CPW * w + c) * Ki + s * Di + p * kSlice) * 4 + 16 * lane : M * Ki * 4,
+                                 0, 0));
             }
             gv[s] = __builtin_bit_cast(
-                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(gamR, (s * Di + p * kSlice) * 4 + 16 * lane, 0, 0));
+                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                             gamR, laneLive ? (s * Di + p * kSlice) * 4 + 16 * lane : Ki * 4, 0, 0));
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -752,7 +762,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     auto load_x_part = [&](auto pc) __attribute__((always_inline)) {
         constexpr int part = decltype(pc)::value;
         constexpr int b = part / 2;
-        const __amdgpu_buffer_rsrc_t r = make_rsrc(x_tile(b), rows_of(b) * Ki * 2);
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(x_tile(b), stripLive ? rows_of(b) * Ki * 2 : 0);
 #pragma unroll
         for (int s = 2 * (part % 2); s < 2 * (part % 2) + 2; ++s) {
 #pragma unroll
@@ -961,7 +971,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
                               bcastAll, (slot_of(jpc) * RC::BWORDS + lane) * 8, 0, kCpolDev));
         }
         {
-            const __amdgpu_buffer_rsrc_t hr = make_rsrc(h_tile(jh), liveH ? rows_of(jh) * Di * 2 : 0);
+            const __amdgpu_buffer_rsrc_t hr = make_rsrc(h_tile(jh), liveH && stripLive ? rows_of(jh) * Di * 2 : 0);
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 store16<kCpolNt>(hout[h], hr, hLane + 8 * h * Di * 2);
@@ -980,7 +990,7 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         //    two loads of that stream of own tile jh + L go out into the
         //    slot hIn just consumed.
         const int jn = jh + L;
-        const __amdgpu_buffer_rsrc_t xr = make_rsrc(x_tile(jn), rows_of(jn) * Ki * 2);
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(x_tile(jn), stripLive ? rows_of(jn) * Ki * 2 : 0);
         f32x4_t acc[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {

@@ -219,6 +219,15 @@ def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_ga
     (777, 3840, True, True),         # P = 15: 13 teams across XCDs
     (1234, 4352, False, False),      # P = 17: 12 teams across XCDs, reducers sized for 32 slices
     (2222, 4864, True, False),       # P = 19: 11 teams across XCDs
+    # D % 256 != 0: the last slice has 1-3 strips of columns, the others
+    # load zeros and store nothing
+    (300, 448, True, True),          # P = 2, the last slice three strips
+    (1000 + 3, 192, False, True),    # one slice, three live strips
+    (2048, 320, True, False),        # P = 2, the last slice one strip
+    (777, 1216, False, False),       # P = 5, the last slice three strips
+    (1500, 4160, True, True),        # P = 17 across XCDs, the last slice one strip
+    (3000 + 1, 7104, True, True),    # P = 28 in an XCD, the last slice three strips
+    (600, 8000, False, True),        # P = 32 across XCDs, the last slice one strip
 ])
 def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
     """Team geometries of the strip kernel on a device of 8 XCDs x 32 CUs:

@@ -307,9 +307,13 @@ def _path(pkg, lib, d, env=None):
     (4, 16640, 4096, "rows"),  # 65 slices: rows
     (4, 64, 4096, "split"),    # n = 4, not a strip width: split for K <= 8704 from T = 2048
     (4, 64, 2047, "rows"),
-    (4, 2176, 2048, "split"),  # K = 8704
-    (4, 2240, 2048, "rows"),   # K = 8960: rows, not fused
-    (4, 7104, 8192, "rows"),
+    (4, 2176, 2048, "strip"),  # D % 64 == 0: strip, the last slice two strips wide
+    (4, 192, 8192, "strip"),   # one slice, three strips
+    (4, 128, 8192, "split"),   # one slice of two strips: not a strip width
+    (4, 2240, 2048, "strip"),
+    (4, 2272, 2048, "rows"),   # D % 64 != 0, K = 9088 > 8704: rows, not fused
+    (4, 7104, 8192, "strip"),
+    (4, 7072, 8192, "rows"),   # D % 64 != 0
     (4, 48, 64, "split"),      # n = 4, D % 64 != 0
     (4, 5120, 128, "rows"),    # small n = 4 batch: T <= 128 at every width
     (4, 256, 128, "rows"),

@@ -186,6 +186,8 @@ def _check_oracle(orc, host, outs, bf16):
     (1000, 4, 7936, False, False, None, "strip"),
     (1500, 4, 8192, False, True, None, "strip"),     # 32 slices
     (600, 4, 16384, True, True, None, "strip"),      # 64 slices
+    (700, 4, 4160, True, True, "strip", "strip"),    # D % 256 != 0: the last slice one strip wide
+    (700, 4, 7104, False, True, "strip", "strip"),   # ... three strips wide
     (2048, 4, 7936, True, True, "fused", "fused"),   # the fused kernel (a fallback)
 ])
 def test_prepared_matches_plain(pkg, orc, device, T, n, D, bf16, gamma_on, force, path):
