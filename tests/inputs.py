@@ -113,6 +113,8 @@ EXTREMES = {
     "n4_D16384_T4096": Case(n=4, D=16384, T=4096, is_bf16=True, gamma=True, seed=20261302),
     "n6_D16384_T4096": Case(n=6, D=16384, T=4096, is_bf16=False, gamma=True, seed=20261303),
     "n4_D7168_B4_S32768": Case(n=4, D=7168, T=131072, is_bf16=True, gamma=True, seed=20261304),
+    # a width with a partial last strip slice (27 slices of 256 columns and one of 192)
+    "n4_D7104_T8192": Case(n=4, D=7104, T=8192, is_bf16=True, gamma=True, seed=20261305),
 }
 EXTREME_LEAD = {"n4_D7168_B4_S32768": (4, 32768)}
 
