@@ -496,17 +496,22 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
             }
         }
     }
-    // Strip path (n = 4, D % 64 == 0 from D = 192): slices of 256 columns
-    // (the last one 64, 128 or 192 wide when D % 256 != 0), at most
-    // strip_max_slices() of them; its tile and row indices are 32-bit, which
-    // bounds T.  Measured on MI355X (bf16, gamma, back to back, us, strip /
-    // rows / split): T = 8192: D = 7104 107.4 / 167.5 / 264.6, 4160 75.3 /
-    // 109.0 / 144.2, 2112 47.1 / 65.1 / 65.7, 1216 29.9 / 48.3 / 44.6, 320
-    // 19.3 / 34.4 / 21.6, 192 16.6 / 31.9 / 17.7; T = 2048: D = 7104 33.8 /
-    // 50.7 / 61.1, 1216 14.4 / 21.4 / 19.1, 192 10.2 / 13.7 / 11.7.  One
-    // slice of one or two strips gains nothing on the split path (D = 64,
-    // T = 8192 16.0 / 27.3 / 15.0; D = 128 16.2 / 31.8 / 15.9).
-    if (n == 4 && (D % 64) == 0 && D >= 192 && (D + 255) / 256 <= mhc::strip_max_slices() &&
+    // Strip path (n = 4, D % 32 == 0 from D = 192): slices of 256 columns
+    // (the last one narrower when D % 256 != 0: whole 64-column strips past
+    // D and, when D % 64 == 32, the upper half of the last live strip load
+    // and store nothing), at most strip_max_slices() of them; its tile and
+    // row indices are 32-bit, which bounds T.  Measured on MI355X (bf16,
+    // gamma, back to back, us, strip / rows / split): T = 8192: D = 7104
+    // 107.4 / 167.5 / 264.6, 7072 122.4 / 168.1 / 261.9 (its odd streams'
+    // rows start half a cache line off), 4160 75.3 / 109.0 / 144.2, 2112
+    // 47.1 / 65.1 / 65.7, 1216 29.9 / 48.3 / 44.6, 320 19.3 / 34.4 / 21.6,
+    // 224 17.4 / 32.8 / 18.5, 192 16.6 / 31.9 / 17.7; T = 2048: D = 7104
+    // 33.8 / 50.7 / 61.1, 7072 37.1 / 50.9 / 60.9, 1216 14.4 / 21.4 / 19.1,
+    // 192 10.2 / 13.7 / 11.7; T = 1024: D = 7072 22.6 / 29.9 / 40.6, 224
+    // 10.3 / 10.7 / 12.0.  One slice of one or two strips gains nothing on
+    // the split path (D = 64, T = 8192 16.0 / 27.3 / 15.0; D = 128 16.2 /
+    // 31.8 / 15.9).
+    if (n == 4 && (D % 32) == 0 && D >= 192 && (D + 255) / 256 <= mhc::strip_max_slices() &&
         T < (int64_t{1} << 24)) {
         p.stripP = static_cast<int>((D + 255) / 256);
     }
@@ -597,7 +602,7 @@ int validate_and_plan(const mhcTensor *x, const mhcTensor *phi, const mhcTensor 
         }
     }
     if (n == 4) {
-        // The strip kernel where it applies (D % 64 == 0, D >= 192), except small
+        // The strip kernel where it applies (D % 32 == 0, D >= 192), except small
         // batches: its fixed cost (every workgroup builds its B slice) is
         // ~11-12 us whatever the shape, while the rows path's two short
         // launches grow with K and T.  Measured on MI355X (back to back, us,

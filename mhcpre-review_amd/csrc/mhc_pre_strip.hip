@@ -1,11 +1,11 @@
-// Strip kernel for gfx950 (n = 4, D % 64 == 0): x is read from HBM once,
+// Strip kernel for gfx950 (n = 4, D % 32 == 0): x is read from HBM once,
 // held in VGPRs in a ring of row tiles until its hIn is written, and the
 // cross-workgroup exchange of the K-reduction runs in the shadow of the x
 // stream.
 //
 // Teams.  The workgroups of one XCD form teams of P = ceil(D / 256) slice
-// workgroups and R reducer workgroups (the last slice's strips past D, when
-// D % 256 != 0, load zeros and store nothing).  Workgroup g runs on XCD g mod X (the
+// workgroups and R reducer workgroups (when D % 256 != 0, the lanes of the
+// last slice whose columns lie past D load zeros and store nothing).  Workgroup g runs on XCD g mod X (the
 // hardware dispatches workgroups round-robin over the X XCDs), so a team's
 // exchange stays inside one XCD's L2.  Results do not depend on where a
 // workgroup actually runs (one placed off its team's XCD writes through to
@@ -630,8 +630,12 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
     const bool stripLive = col0 < Di;
     const int lrow = lane & 7;
     const int lineOff = 8 * (lane >> 4) + 32 * ((lane >> 3) & 1);
-    const int xLane = (lrow * Ki + col0 + lineOff) * 2;
-    const int hLane = (lrow * Di + col0 + lineOff) * 2;
+    // A lane whose 8 columns lie past D (the last slice when D % 64 != 0)
+    // loads and stores nothing: its offsets are past every resource's end.
+    constexpr int kPastEnd = 0x40000000;
+    const bool colLive = col0 + lineOff < Di;
+    const int xLane = colLive ? (lrow * Ki + col0 + lineOff) * 2 : kPastEnd;
+    const int hLane = colLive ? (lrow * Di + col0 + lineOff) * 2 : kPastEnd;
     const int rl = lane & 15;
     const int grp = lane >> 4;
     if (tid < kGroups) {
@@ -718,9 +722,10 @@ __global__ __launch_bounds__(kWaves * 64) void strip_kernel(StripArgs a)
         for (int i = 0; i < KW; ++i) {
             const int ks = half + kGroups * i;
             const int64_t gks = ((int64_t)(ks >> 1) * a.D + col0 + 32 * (ks & 1)) / 32;
+            const bool ksLive = col0 + 32 * (ks & 1) < Di;  // the k-step's 32 columns are within D
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                pf[i][t] = stripLive ? a.bprep[(gks * NT + t) * 64 + lane] : u32x4_t{0u, 0u, 0u, 0u};
+                pf[i][t] = ksLive ? a.bprep[(gks * NT + t) * 64 + lane] : u32x4_t{0u, 0u, 0u, 0u};
             }
         }
     } else {

@@ -228,6 +228,12 @@ def test_ragged_rows_and_small_widths(pkg, orc, device, T, n, D, is_bf16, has_ga
     (1500, 4160, True, True),        # P = 17 across XCDs, the last slice one strip
     (3000 + 1, 7104, True, True),    # P = 28 in an XCD, the last slice three strips
     (600, 8000, False, True),        # P = 32 across XCDs, the last slice one strip
+    # D % 64 == 32: the last live strip has 32 columns, its other lanes load
+    # and store nothing
+    (500, 224, True, True),          # one slice of 3.5 strips
+    (1111, 480, False, True),        # P = 2
+    (2000, 2272, True, False),       # P = 9 across XCDs
+    (3000 + 1, 7072, True, True),    # P = 28, the last slice 2.5 strips
 ])
 def test_strip_team_shapes(pkg, orc, device, T, D, is_bf16, has_gamma):
     """Team geometries of the strip kernel on a device of 8 XCDs x 32 CUs:

@@ -311,9 +311,11 @@ def _path(pkg, lib, d, env=None):
     (4, 192, 8192, "strip"),   # one slice, three strips
     (4, 128, 8192, "split"),   # one slice of two strips: not a strip width
     (4, 2240, 2048, "strip"),
-    (4, 2272, 2048, "rows"),   # D % 64 != 0, K = 9088 > 8704: rows, not fused
+    (4, 2272, 2048, "strip"),  # D % 64 == 32: strip, the last strip half live
+    (4, 2256, 2048, "split"),  # D % 32 != 0: K % 128 != 0, split
     (4, 7104, 8192, "strip"),
-    (4, 7072, 8192, "rows"),   # D % 64 != 0
+    (4, 7072, 8192, "strip"),
+    (4, 7056, 8192, "split"),  # D % 32 != 0
     (4, 48, 64, "split"),      # n = 4, D % 64 != 0
     (4, 5120, 128, "rows"),    # small n = 4 batch: T <= 128 at every width
     (4, 256, 128, "rows"),

@@ -188,6 +188,7 @@ def _check_oracle(orc, host, outs, bf16):
     (600, 4, 16384, True, True, None, "strip"),      # 64 slices
     (700, 4, 4160, True, True, "strip", "strip"),    # D % 256 != 0: the last slice one strip wide
     (700, 4, 7104, False, True, "strip", "strip"),   # ... three strips wide
+    (700, 4, 7072, True, True, "strip", "strip"),    # ... two and a half strips
     (2048, 4, 7936, True, True, "fused", "fused"),   # the fused kernel (a fallback)
 ])
 def test_prepared_matches_plain(pkg, orc, device, T, n, D, bf16, gamma_on, force, path):
