@@ -15,12 +15,12 @@ import numpy as np
 ROOT = Path(__file__).resolve().parents[2]
 sys.path[:0] = [str(ROOT), str(ROOT / "tests")]
 
-from inputs import CONFIGS, make_case  # noqa: E402
+from inputs import WORKLOADS, make_case  # noqa: E402
 from oracle import oracle  # noqa: E402
 
 
 def main() -> None:
-    case = CONFIGS[1]
+    case = WORKLOADS[1]
     x, phi, alpha, bias, gamma = make_case(case)
     out = oracle.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
     np.savez_compressed(

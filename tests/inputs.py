@@ -94,7 +94,7 @@ class Case:
 
 
 # The five workloads: plumbing, mid-size, headline prefill, decode, ragged tail.
-CONFIGS = {
+WORKLOADS = {
     1: Case(n=4, D=256, T=128, is_bf16=False, gamma=False, seed=20261201 + 1),
     2: Case(n=4, D=4096, T=1024, is_bf16=True, gamma=True, seed=20261201 + 2),
     3: Case(n=4, D=7168, T=8192, is_bf16=True, gamma=True, seed=20261201 + 3),
@@ -105,9 +105,9 @@ CONFIGS = {
 
 # The reference's legal extremes (audit_group_vec.py:37,41-45,123-146: any
 # D % 16 == 0 up to 16384 for every n, up to B * S = 4 * 32768 rows) at the
-# shapes that stress this build's paths: n = 4 widths past the strip kernel's
-# 31 slices, the widest n = 4 and n = 6 rows, and the headline width over
-# 131072 rows (x passed as [4, 32768, n, D]).
+# shapes that stress the library's paths: n = 4 widths whose strip teams span
+# the XCDs (32 and 64 slices), the widest n = 4 and n = 6 rows, and the
+# headline width over 131072 rows (x passed as [4, 32768, n, D]).
 EXTREMES = {
     "n4_D8192_T8192": Case(n=4, D=8192, T=8192, is_bf16=True, gamma=True, seed=20261301),
     "n4_D16384_T4096": Case(n=4, D=16384, T=4096, is_bf16=True, gamma=True, seed=20261302),

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 from helpers import assert_close_f32, assert_hin
-from inputs import CONFIGS, EXTREME_LEAD, EXTREMES, make_weights, outlier_rows
+from inputs import WORKLOADS, EXTREME_LEAD, EXTREMES, make_weights, outlier_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -49,7 +49,7 @@ def _gpu_inputs(case, device):
 def test_full_size(pkg, orc, device, cfg):
     import torch
 
-    case = CONFIGS[cfg] if cfg in CONFIGS else EXTREMES[cfg]
+    case = WORKLOADS[cfg] if cfg in WORKLOADS else EXTREMES[cfg]
     _say(f"[fullsize] {cfg}: {case}")
     x, phi, alpha, bias, gamma, pt, at, bt, gt, out_rows = _gpu_inputs(case, device)
     lead = EXTREME_LEAD.get(cfg)

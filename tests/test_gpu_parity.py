@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from helpers import assert_close_f32, assert_hin, ulp_distance
-from inputs import (CONFIGS, E3_ALPHA, E3_CASES, audit_formula_case, audit_formula_cases,
+from inputs import (WORKLOADS, E3_ALPHA, E3_CASES, audit_formula_case, audit_formula_cases,
                     make_case, to_bits)
 
 pytestmark = pytest.mark.gpu
@@ -88,7 +88,7 @@ def check(out, ref, x_bits, is_bf16, orc):
                                        (2, "split"), (1, "fused"), (2, "fused"), (1, "rows"),
                                        (2, "rows"), (1, "strip")])
 def test_config_full_parity(pkg, orc, device, cfg, force):
-    case = CONFIGS[cfg]
+    case = WORKLOADS[cfg]
     _say(f"[parity] config {cfg} force={force}: {case}")
     x, phi, alpha, bias, gamma = make_case(case)
     out = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, force_path=force)
@@ -100,7 +100,7 @@ def test_config_full_parity(pkg, orc, device, cfg, force):
 def test_cooperative_launch_matches(pkg, orc, device, force):
     """The cooperative launch mode (MHCPRE_LAUNCH=cooperative) runs the same
     kernel: bit-identical outputs to the default launch, and parity."""
-    case = CONFIGS[2]
+    case = WORKLOADS[2]
     _say(f"[parity] config 2 cooperative launch ({force}): {case}")
     x, phi, alpha, bias, gamma = make_case(case)
     coop = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma, launch="cooperative",
@@ -312,7 +312,7 @@ def test_strip_few_tiles_per_team(pkg, orc, device, T, D, is_bf16, has_gamma):
 def test_attributes_and_hpre_off(pkg, orc, device):
     """Non-default normEps/hcEps (hcEps = 0 skips the add, mhc_pre.cpp:552) and the
     3-output entry point (no hPre)."""
-    case = CONFIGS[1]
+    case = WORKLOADS[1]
     x, phi, alpha, bias, _ = make_case(case)
     for norm_eps, hc_eps in ((1e-3, 0.0), (0.5, 0.25)):
         out = run_gpu(pkg, device, x, case.is_bf16, phi, alpha, bias, None, norm_eps, hc_eps,
@@ -343,7 +343,7 @@ def test_determinism(pkg, device, cfg):
     """Two launches give bitwise-identical outputs (fixed-order reductions, no atomics)."""
     import torch
 
-    case = CONFIGS[cfg]
+    case = WORKLOADS[cfg]
     x, phi, alpha, bias, gamma = make_case(case)
     xt, pt, at, bt, gt = to_device(pkg, device, x, case.is_bf16, phi, alpha, bias, gamma)
     op = pkg.MhcPreOp(xt, pt, at, bt, gt, h_pre=True)

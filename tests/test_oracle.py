@@ -17,7 +17,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from inputs import (CONFIGS, E3_ALPHA, audit_formula_case, audit_formula_cases, make_case,
+from inputs import (WORKLOADS, E3_ALPHA, audit_formula_case, audit_formula_cases, make_case,
                     to_bits)
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -298,7 +298,7 @@ def test_audit_formula_ranges(orc, case):
 
 
 def test_rows_subset_and_threads_are_exact(orc):
-    case = CONFIGS[1]
+    case = WORKLOADS[1]
     x, phi, alpha, bias, gamma = make_case(case)
     full = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma, nthreads=1)
     rows = [127, 0, 64, 3]
@@ -310,7 +310,7 @@ def test_rows_subset_and_threads_are_exact(orc):
 def test_golden_fixture_config1(orc):
     """Regression pin: the committed config-1 outputs (tests/golden/make_golden.py)."""
     data = np.load(GOLDEN / "config1_oracle.npz")
-    case = CONFIGS[1]
+    case = WORKLOADS[1]
     x, phi, alpha, bias, gamma = make_case(case)
     import hashlib
 
@@ -324,7 +324,7 @@ def test_weighted_stream_sum_is_the_oracle_hin_stage(orc):
     """oracle.weighted_stream_sum on the oracle's own hPre reproduces its hIn bit
     for bit (the GPU tests use it to check the device's hIn stage exactly)."""
     for cfg in (1, 2):
-        case = CONFIGS[cfg]
+        case = WORKLOADS[cfg]
         x, phi, alpha, bias, gamma = make_case(case)
         x = x[:64]
         out = orc.mhc_pre(x, case.is_bf16, phi, alpha, bias, gamma)
