@@ -99,7 +99,7 @@ typedef struct mhcPreExecutor mhcPreExecutor;
  * On success *workspaceSize holds the bytes the caller must allocate and
  * *executor a new executor (free it with mhcPreExecutorDestroy).  The size is
  * that of the launch path the plan takes.  On the strip path (n = 4, D a
- * multiple of 256 up to 7936, all but small batches) it holds per-team
+ * multiple of 32 from 192 up to 16384, all but small batches) it holds per-team
  * exchange rings only and does not grow with T (7.2 MB at n = 4, D = 7168);
  * the team count is that of the device holding x (of MI355X when the runtime
  * cannot tell).  The two-pass paths hold partial sums that grow with T.

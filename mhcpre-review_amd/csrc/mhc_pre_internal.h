@@ -76,10 +76,10 @@ struct Plan {
     int fusedTeams = 0;       // teams of fusedP workgroups
     int64_t fusedTiles = 0;   // 16-row tiles
 
-    // Strip path (n = 4, D % 256 == 0): P slice workgroups of 256 columns and
-    // R reducer workgroups per team, teams formed inside one XCD.  stripR,
-    // stripXcds, stripTeamsPerXcd and stripGrid are filled per launch from
-    // the device.
+    // Strip path (n = 4, D % 32 == 0 from D = 192): P = ceil(D / 256) slice
+    // workgroups of 256 columns and R reducer workgroups per team, teams
+    // formed inside one XCD or across the device.  stripR, stripXcds,
+    // stripTeamsPerXcd and stripGrid are filled per launch from the device.
     int stripP = 0;
     int stripMaxTeams = 0;  // teams the workspace's exchange rings are sized for (those of the
                             // device phase 1 planned for)

@@ -115,7 +115,7 @@ struct StripArgs {
     int64_t D;
     int64_t K;
     int64_t RT;
-    int P;            // slice workgroups per team (D / 256)
+    int P;            // slice workgroups per team (ceil(D / 256))
     int R;            // reducer workgroups per team
     int nXcd;         // XCDs of the device
     int teamsPerXcd;  // teams formed from the workgroups of one XCD

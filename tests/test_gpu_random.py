@@ -39,8 +39,9 @@ MAX_ELEMS = 6_000_000  # T * n * D per case
 def random_case(i: int):
     rng = np.random.default_rng(0x5EED0000 + SEED_BASE + i)
     n = int(rng.choice([4, 6, 8]))
-    # Widths that reach every path: multiples of 256 (strip), of 64 (fused),
-    # of 128 / n (rows), and of 16 only (split).
+    # Widths that reach every path: multiples of 256 (strip, whole slices),
+    # of 64 (strip with a partial last slice, or fused), of 128 / n (rows),
+    # and of 16 only (split).
     kind = int(rng.integers(0, 4))
     if kind == 0:
         D = 256 * int(rng.integers(1, 32))

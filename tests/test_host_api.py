@@ -295,7 +295,7 @@ def _path(pkg, lib, d, env=None):
 
 
 @pytest.mark.parametrize("n,D,S,want", [
-    (4, 7168, 4096, "strip"),  # D % 256 == 0, D / 256 <= 31
+    (4, 7168, 4096, "strip"),  # 28 slices of 256 columns, one team per XCD
     (4, 7680, 8192, "strip"),  # 30 slices and 2 reducers per XCD
     (4, 7936, 8192, "strip"),  # 31 or more slices: teams across XCDs
     (4, 7936, 1025, "strip"),
